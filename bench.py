@@ -1,0 +1,347 @@
+"""Benchmark of the MI355X attention path (one GPU).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+
+Headline (`value`): BASELINE.json configs[1] — dense causal FlashAttention
+forward + backward, fp16, q/k/v/dO [B=4, S=2048, H=16, D=128], one step =
+tilelang_flash_attn_func forward + autograd backward over resident inputs.
+value = algorithmic FLOPs per step / step time (FLOPs over unmasked pairs
+only: fwd 4*D*H*pairs, bwd 2.5x fwd).
+
+`roofline` covers the dominant launch of that step, the fa_bwd call (its
+pre / main / dQ-convert kernels), timed with HIP events on the stream it is
+launched on.  `extra` reports the other BASELINE configs and the north-star
+points (T1: S=8192 fwd+bwd, T2: decode at 32k context) with their own
+roofline fractions; paged/decode reps flush the 256 MB Infinity Cache.
+`cpu_baseline` times the CPU oracle (fp32 PyTorch math, the reference math
+path) on a bounded sample of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "tilelang-fa-v100_amd"))
+sys.path.insert(0, REPO)
+
+import torch  # noqa: E402
+
+PEAK_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA
+PEAK_GBS = 8000.0     # MI355X HBM3E
+METRIC = "attn TFLOP/s (prefill/bwd) + decode KV GB/s, % of MI355X roofline, 1 GPU"
+
+
+# --------------------------------------------------------------------- workloads
+# Seeded recipe: CPU generator per config, lengths first, then the page
+# permutation, then q, k, v (then dO); N(0,1) in fp32 cast to the dtype.
+
+def dense_inputs(B, S, H, D, dtype, device, seed=0, with_do=True):
+    g = torch.Generator().manual_seed(seed)
+    ts = [torch.randn(B, S, H, D, generator=g).to(dtype) for _ in range(4 if with_do else 3)]
+    return [t.to(device) for t in ts]
+
+
+def dense_pairs(sq, sk, causal):
+    if not causal:
+        return sq * sk
+    off = sk - sq
+    # sum_i clamp(i + off + 1, 0, sk)
+    return sum(max(0, min(i + off + 1, sk)) for i in range(sq))
+
+
+def paged_inputs(lens_q, lens_kv, prefixes, Hq, Hkv, D, dtype, device, g, page=16,
+                 device_values=False):
+    """Scattered-page cache (pool = sum of pages), block table padded with -1."""
+    npg = [math.ceil(n / page) for n in lens_kv]
+    pool = sum(npg)
+    perm = torch.randperm(pool, generator=g)
+    maxb = max(npg)
+    bt = torch.full((len(lens_kv), maxb), -1, dtype=torch.int32)
+    cur = 0
+    for b, n in enumerate(npg):
+        bt[b, :n] = perm[cur:cur + n].to(torch.int32)
+        cur += n
+    T = sum(lens_q)
+    if device_values:
+        gd = torch.Generator(device=device).manual_seed(0)
+        mk = lambda *s: torch.randn(*s, generator=gd, device=device, dtype=torch.float32).to(dtype)  # noqa: E731
+        q = mk(T, Hq, D)
+        kc = mk(pool, page, Hkv, D)
+        vc = mk(pool, page, Hkv, D)
+    else:
+        q = torch.randn(T, Hq, D, generator=g).to(dtype).to(device)
+        kc = torch.randn(pool, page, Hkv, D, generator=g).to(dtype).to(device)
+        vc = torch.randn(pool, page, Hkv, D, generator=g).to(dtype).to(device)
+    qsl = torch.tensor([0] + torch.tensor(lens_q).cumsum(0).tolist(), dtype=torch.int32)
+    return dict(q=q, k_cache=kc, v_cache=vc, block_table=bt.to(device),
+                seq_lens=torch.tensor(lens_kv, dtype=torch.int32, device=device),
+                query_start_loc=qsl.to(device),
+                prefix_kv_lens=torch.tensor(prefixes, dtype=torch.int32, device=device))
+
+
+def c3_lens():
+    g = torch.Generator().manual_seed(0)
+    return torch.randint(512, 4097, (8,), generator=g).tolist(), g
+
+
+def c4_lens():
+    g = torch.Generator().manual_seed(0)
+    return torch.randint(1024, 32769, (64,), generator=g).tolist(), g
+
+
+def c5_prefix():
+    g = torch.Generator().manual_seed(0)
+    return torch.randint(0, 8193, (16,), generator=g).tolist(), g
+
+
+def decode_bytes(lens, Hq, Hkv, D, page=16, elem=2):
+    kv = sum(lens) * Hkv * D * 2 * elem
+    qo = len(lens) * Hq * D * elem * 2
+    bt = sum(math.ceil(n / page) for n in lens) * 4 + 4 * len(lens)
+    return kv + qo + bt
+
+
+# --------------------------------------------------------------------- timing
+
+class CacheFlush:
+    """Overwrites a 512 MB buffer so the 256 MB Infinity Cache holds no inputs."""
+
+    def __init__(self, device):
+        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+
+    def __call__(self):
+        self.buf.fill_(1)
+
+
+def time_reps(fn, reps, warmup, flush=None):
+    """Median per-call time (ms) from HIP events around each call."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        if flush is not None:
+            flush()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times), times
+
+
+def flop_entry(name, flops, ms, extra=None):
+    tf = flops / (ms * 1e-3) / 1e12
+    d = {"ms": round(ms, 4), "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
+         "frac_of_peak": round(tf / PEAK_TFLOPS, 4)}
+    if extra:
+        d.update(extra)
+    return name, d
+
+
+def bytes_entry(name, nbytes, ms, extra=None):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    d = {"ms": round(ms, 4), "gbytes": round(nbytes / 1e9, 3), "gbs": round(gbs, 1),
+         "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    if extra:
+        d.update(extra)
+    return name, d
+
+
+# --------------------------------------------------------------------- legs
+
+def headline(fa, steps, warmup, dev):
+    B, S, H, D = 4, 2048, 16, 128
+    q, k, v, do = dense_inputs(B, S, H, D, torch.float16, dev)
+    q.requires_grad_()
+    k.requires_grad_()
+    v.requires_grad_()
+    pairs = dense_pairs(S, S, True)
+    f_fwd = 4 * D * H * pairs * B
+    f_step = 3.5 * f_fwd
+
+    def step():
+        out = fa.tilelang_flash_attn_func(q, k, v, causal=True)
+        out.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        step()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+
+    # Dominant launch: fa_bwd (pre + main + dQ convert) through the C ABI.
+    from tilelang_fa_v100 import _dense, _lib
+    qd, kd, vd = q.detach(), k.detach(), v.detach()
+    out, lse = _dense.forward(qd, kd, vd, D ** -0.5, True)
+    dq, dk, dv = (torch.empty_like(t) for t in (qd, kd, vd))
+    a = _dense.bwd_args(qd, kd, vd, out, do, lse, dq, dk, dv, D ** -0.5, True, False)
+    lib = _lib.load()
+    nbytes = lib.fa_bwd_workspace_bytes(ctypes.byref(a))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(qd.device)
+
+    def bwd():
+        _lib.check(lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), nbytes, stream), "fa_bwd")
+
+    bwd_ms, _ = time_reps(bwd, max(steps, 20), 3)
+    fwd_ms, _ = time_reps(lambda: _dense.forward(qd, kd, vd, D ** -0.5, True), max(steps, 20), 3)
+    bwd_tf = 2.5 * f_fwd / (bwd_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(bwd_tf, 1), "peak": PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(bwd_tf / PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "fa_bwd (bwd_pre + bwd_main + bwd_dq_convert)",
+                "launch_ms": round(bwd_ms, 4), "algorithmic_gflop": round(2.5 * f_fwd / 1e9, 2)}
+    parts = dict([flop_entry("C2_fwd", f_fwd, fwd_ms), flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms)])
+    return ms, f_step, roofline, parts
+
+
+def extras(fa, dev, reps):
+    res = {}
+    flush = CacheFlush(dev)
+    # C1: dense non-causal forward fp16 [1,512,16,64]
+    q, k, v = dense_inputs(1, 512, 16, 64, torch.float16, dev, with_do=False)
+    ms, _ = time_reps(lambda: fa.tilelang_flash_attn_func(q, k, v), reps, 5)
+    res.update([flop_entry("C1_fwd", 4 * 64 * 16 * 512 * 512, ms)])
+
+    # T1: dense causal fwd+bwd S=8192 D=128, B=2 H=16
+    q, k, v, do = dense_inputs(2, 8192, 16, 128, torch.float16, dev)
+    for t in (q, k, v):
+        t.requires_grad_()
+    f_fwd = 4 * 128 * 16 * dense_pairs(8192, 8192, True) * 2
+
+    def t1():
+        o = fa.tilelang_flash_attn_func(q, k, v, causal=True)
+        o.backward(do)
+
+    ms, _ = time_reps(t1, max(reps // 2, 5), 2)
+    res.update([flop_entry("T1_fwd_bwd", 3.5 * f_fwd, ms)])
+    ms, _ = time_reps(lambda: fa.tilelang_flash_attn_func(q.detach(), k.detach(), v.detach(),
+                                                          causal=True), reps, 3)
+    res.update([flop_entry("T1_fwd", f_fwd, ms)])
+    del q, k, v, do
+
+    # C3: paged causal prefill fp16, 8 seqs U[512,4096], 32/8 heads, D=128
+    lens, g = c3_lens()
+    c = paged_inputs(lens, lens, [0] * 8, 32, 8, 128, torch.float16, dev, g)
+    pairs = sum(n * (n + 1) // 2 for n in lens)
+    run = lambda: fa.tilelang_paged_forward(**c)  # noqa: E731
+    ms, _ = time_reps(run, reps, 3, flush)
+    res.update([flop_entry("C3_paged_prefill", 4 * 128 * 32 * pairs, ms)])
+    del c
+
+    # C5: chunked prefill with prefix, bf16, 16 x 512 new tokens, 64/8 heads
+    pf, g = c5_prefix()
+    c = paged_inputs([512] * 16, [p + 512 for p in pf], pf, 64, 8, 128, torch.bfloat16, dev, g)
+    pairs = sum(sum(min(p + t + 1, p + 512) for t in range(512)) for p in pf)
+    run = lambda: fa.tilelang_paged_forward(**c)  # noqa: E731
+    ms, _ = time_reps(run, reps, 3, flush)
+    res.update([flop_entry("C5_chunked_prefill_bf16", 4 * 128 * 64 * pairs, ms)])
+    del c
+
+    # C4 / T2: paged decode, batch 64, 32/8 heads, D=128
+    for name, lens_fn in (("C4_decode", lambda: c4_lens()),
+                          ("T2_decode_32k", lambda: ([32768] * 64, torch.Generator().manual_seed(0)))):
+        lens, g = lens_fn()
+        c = paged_inputs([1] * 64, lens, [0] * 64, 32, 8, 128, torch.float16, dev, g,
+                         device_values=True)
+        qd = c["q"].view(64, 32, 128)
+        run = lambda: fa.tilelang_decode_forward(qd, c["k_cache"], c["v_cache"],  # noqa: E731
+                                                 c["block_table"], c["seq_lens"])
+        ms, _ = time_reps(run, reps, 3, flush)
+        res.update([bytes_entry(name, decode_bytes(lens, 32, 8, 128), ms)])
+        del c, qd
+    return res
+
+
+def cpu_baseline(budget_s=12.0):
+    """Oracle fp32 fwd+bwd on C2 heads, one (b, h) at a time, for ~budget_s."""
+    from oracle import attention_ref as ref
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    B, S, H, D = 4, 2048, 16, 128
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(1, S, 1, D, generator=g).half() for _ in range(4))
+    per_head = 3.5 * 4 * D * dense_pairs(S, S, True)
+    ref.dense_attention(q, k, v, causal=True)  # warm-up
+    done, t0 = 0, time.perf_counter()
+    while True:
+        ref.dense_attention(q, k, v, causal=True)
+        ref.dense_attention_backward(q, k, v, do, causal=True)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= B * H:
+            break
+    tf = done * per_head / el / 1e12
+    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"C2 fwd+bwd, {done} of {B * H} (batch, head) slices, fp32 oracle "
+                      f"(oracle/attention_ref.py) on CPU, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    import tilelang_fa_v100 as fa
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    print(f"[bench] headline C2: warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
+    ms, f_step, roof, parts = headline(fa, args.steps, args.warmup, dev)
+    extra = dict(parts)
+    if not args.no_extra:
+        print("[bench] extra configs", file=sys.stderr, flush=True)
+        extra.update(extras(fa, dev, args.reps))
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(f_step / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "C2: dense causal FA fwd+bwd, fp16, q/k/v/dO [4,2048,16,128], "
+                               "seed 0, scale 1/sqrt(128)",
+                   "global_batch": 4, "seq_len": 2048, "heads": 16, "head_dim": 128,
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,268 @@
+"""CPU tests of the drop-in boundary: the C ABI library and the Python API.
+
+No GPU is needed: the library loads in a CPU-only process and every argument
+check runs before any HIP call, so rejected calls are observable here.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+import tilelang_fa_v100 as fa
+from tilelang_fa_v100 import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fa355.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\*?\s+\*?(fa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_function():
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib._PROTOTYPES), "ctypes prototypes out of sync with header"
+
+
+def test_abi_version_and_strerror():
+    lib = _lib.load()
+    assert lib.fa_abi_version() == _lib.ABI_VERSION
+    for code in (_lib.FA_OK, _lib.FA_E_INVALID, _lib.FA_E_UNSUPPORTED, _lib.FA_E_HIP,
+                 _lib.FA_E_WORKSPACE):
+        assert lib.fa_strerror(code)
+    assert lib.fa_strerror(-99) == b"unknown status"
+
+
+STRUCTS = {"fa_fwd_args": _lib.FwdArgs, "fa_bwd_args": _lib.BwdArgs,
+           "fa_paged_args": _lib.PagedArgs, "fa_decode_args": _lib.DecodeArgs}
+
+
+def test_ctypes_structs_match_c_layout(tmp_path):
+    """Compiles a C program against the header and compares sizeof/offsetof."""
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "fa355.h"', "int main(void){"]
+    for cname, py in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{os.path.dirname(HEADER)}", str(src), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    for line in out.splitlines():
+        cname, field, val = line.split()
+        py = STRUCTS[cname]
+        if field == "size":
+            assert ctypes.sizeof(py) == int(val), cname
+        else:
+            assert getattr(py, field).offset == int(val), (cname, field)
+
+
+def fwd_args(**over):
+    a = _lib.FwdArgs()
+    a.q = a.k = a.v = a.out = 0x1000
+    a.lse = 0
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[:] = (512 * 16 * 128, 16 * 128, 128)
+    a.batch, a.seqlen_q, a.seqlen_k, a.num_heads, a.num_heads_k, a.head_dim = 1, 512, 512, 16, 16, 128
+    a.softmax_scale, a.causal, a.dtype = 0.088, 1, 0
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(q=None), _lib.FA_E_INVALID),
+    (dict(dtype=7), _lib.FA_E_UNSUPPORTED),
+    (dict(head_dim=96), _lib.FA_E_UNSUPPORTED),
+    (dict(num_heads_k=5), _lib.FA_E_INVALID),
+    (dict(seqlen_q=-1), _lib.FA_E_INVALID),
+    (dict(q=0x1008), _lib.FA_E_UNSUPPORTED),  # not 16-byte aligned
+])
+def test_fwd_rejects_bad_arguments(over, status):
+    lib = _lib.load()
+    assert lib.fa_fwd(ctypes.byref(fwd_args(**over)), None) == status
+    assert lib.fa_last_error_message()
+
+
+def test_fwd_rejects_unaligned_stride():
+    a = fwd_args()
+    a.k_stride[1] = 130
+    assert _lib.load().fa_fwd(ctypes.byref(a), None) == _lib.FA_E_UNSUPPORTED
+
+
+def bwd_args(**over):
+    a = _lib.BwdArgs()
+    for n in ("q", "k", "v", "out", "dout", "lse", "dq", "dk", "dv"):
+        setattr(a, n, 0x2000)
+    for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv"):
+        getattr(a, f"{n}_stride")[:] = (2048 * 16 * 128, 16 * 128, 128)
+    a.batch, a.seqlen_q, a.seqlen_k, a.num_heads, a.num_heads_k, a.head_dim = 4, 2048, 2048, 16, 16, 128
+    a.softmax_scale, a.causal, a.dtype = 0.088, 1, 0
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_bwd_workspace_size_and_checks():
+    lib = _lib.load()
+    a = bwd_args()
+    rows = 4 * 2048 * 16
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == rows * 128 * 4 + 2 * rows * 4 + 256
+    # workspace missing / too small is rejected before any launch
+    assert lib.fa_bwd(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE
+    assert lib.fa_bwd(ctypes.byref(a), 0x4000, 16, None) == _lib.FA_E_WORKSPACE
+    assert lib.fa_bwd(ctypes.byref(bwd_args(head_dim=256)), 0x4000, 1 << 40, None) == \
+        _lib.FA_E_UNSUPPORTED
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(bwd_args(lse=None))) == 0
+
+
+def paged_args(**over):
+    a = _lib.PagedArgs()
+    for n in ("q", "k_cache", "v_cache", "out", "block_table", "seq_lens", "query_start_loc",
+              "prefix_kv_lens"):
+        setattr(a, n, 0x3000)
+    a.q_stride[:] = (32 * 128, 128)
+    a.o_stride[:] = (32 * 128, 128)
+    a.k_stride[:] = (16 * 8 * 128, 8 * 128, 128)
+    a.v_stride[:] = (16 * 8 * 128, 8 * 128, 128)
+    a.block_table_stride, a.max_blocks = 300, 237
+    a.num_tokens, a.batch, a.num_heads, a.num_kv_heads, a.head_dim = 19679, 8, 32, 8, 128
+    a.page_size, a.num_pages, a.softmax_scale, a.causal = 16, 1233, 0.088, 1
+    a.window_q = a.window_k = -1
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(block_table=None), _lib.FA_E_INVALID),
+    (dict(page_size=24), _lib.FA_E_UNSUPPORTED),
+    (dict(num_kv_heads=7), _lib.FA_E_INVALID),
+    (dict(block_table_stride=100), _lib.FA_E_INVALID),
+    (dict(head_dim=80), _lib.FA_E_UNSUPPORTED),
+])
+def test_paged_rejects_bad_arguments(over, status):
+    assert _lib.load().fa_paged_prefill(ctypes.byref(paged_args(**over)), None) == status
+
+
+def decode_args(**over):
+    a = _lib.DecodeArgs()
+    for n in ("q", "k_cache", "v_cache", "out", "block_table", "seq_lens"):
+        setattr(a, n, 0x5000)
+    a.q_stride[:] = (32 * 128, 128)
+    a.o_stride[:] = (32 * 128, 128)
+    a.k_stride[:] = (16 * 8 * 128, 8 * 128, 128)
+    a.v_stride[:] = (16 * 8 * 128, 8 * 128, 128)
+    a.block_table_stride, a.max_blocks, a.max_seq_len = 2048, 2048, 32768
+    a.batch, a.num_heads, a.num_kv_heads, a.head_dim = 64, 32, 8, 128
+    a.page_size, a.num_pages, a.softmax_scale = 16, 131072, 0.088
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_decode_workspace_and_checks():
+    lib = _lib.load()
+    a = decode_args()
+    rows = 64 * 32 * (32768 // 256)
+    assert lib.fa_decode_workspace_bytes(ctypes.byref(a)) == rows * 128 * 4 + rows * 4 + 256
+    assert lib.fa_paged_decode(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE
+    assert lib.fa_paged_decode(ctypes.byref(decode_args(max_seq_len=100)), 0x6000, 1 << 40,
+                               None) == _lib.FA_E_INVALID
+    assert lib.fa_paged_decode(ctypes.byref(decode_args(page_size=3)), 0x6000, 1 << 40,
+                               None) == _lib.FA_E_UNSUPPORTED
+
+
+# ------------------------------------------------------------------ Python API
+
+def _qkv(dtype=torch.float16, shape=(1, 8, 2, 64)):
+    return (torch.zeros(shape, dtype=dtype) for _ in range(3))
+
+
+@pytest.mark.parametrize("kw", [dict(dropout_p=0.1), dict(alibi_slopes=torch.zeros(2)),
+                                dict(softcap=1.0)])
+def test_unsupported_features_raise_not_implemented(kw):
+    q, k, v = _qkv()
+    with pytest.raises(NotImplementedError):
+        fa.tilelang_flash_attn_func(q, k, v, **kw)
+
+
+def test_dense_validation_errors():
+    q, k, v = _qkv()
+    with pytest.raises(TypeError):
+        fa.tilelang_flash_attn_func(q.float(), k.float(), v.float())
+    with pytest.raises(TypeError):
+        fa.tilelang_flash_attn_func(q, k.bfloat16(), v)
+    with pytest.raises(ValueError, match="head_dim"):
+        fa.tilelang_flash_attn_func(*_qkv(shape=(1, 8, 2, 96)))
+    with pytest.raises(ValueError, match="multiple"):
+        fa.tilelang_flash_attn_func(torch.zeros(1, 8, 3, 64, dtype=torch.float16), k, v)
+    with pytest.raises(ValueError, match="GPU"):
+        fa.tilelang_flash_attn_func(q, k, v)
+    assert fa.tilelang_flash_attn_gpu is fa.tilelang_flash_attn_func
+
+
+def test_paged_validation_errors():
+    q = torch.zeros(10, 8, 128, dtype=torch.float16)
+    kc = torch.zeros(4, 16, 2, 128, dtype=torch.float16)
+    bt = torch.zeros(2, 2, dtype=torch.int32)
+    sl = torch.tensor([5, 5], dtype=torch.int32)
+    qsl = torch.tensor([0, 5, 10], dtype=torch.int32)
+    pkl = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="block_size"):
+        fa.tilelang_paged_forward(q, kc, kc, bt, sl, qsl, pkl, block_size=32)
+    with pytest.raises(ValueError, match="num_kv_heads"):
+        fa.tilelang_paged_forward(q, kc, kc, bt, sl, qsl, pkl, num_kv_heads=4)
+    with pytest.raises(ValueError, match="multiple"):
+        fa.tilelang_paged_forward(torch.zeros(10, 7, 128, dtype=torch.float16),
+                                  kc, kc, bt, sl, qsl, pkl)
+    with pytest.raises(TypeError):
+        fa.tilelang_paged_forward(q, kc.bfloat16(), kc, bt, sl, qsl, pkl)
+    with pytest.raises(ValueError, match="GPU"):
+        fa.tilelang_paged_forward(q, kc, kc, bt, sl, qsl, pkl)
+
+
+def test_decode_validation_errors():
+    q = torch.zeros(2, 8, 128, dtype=torch.float16)
+    kc = torch.zeros(4, 16, 2, 128, dtype=torch.float16)
+    bt = torch.zeros(2, 2, dtype=torch.int32)
+    sl = torch.tensor([5, 5], dtype=torch.int32)
+    with pytest.raises(ValueError, match="block_size"):
+        fa.tilelang_decode_forward(q, kc, kc, bt, sl, block_size=8)
+    with pytest.raises(ValueError, match="block_table"):
+        fa.tilelang_decode_forward(q, kc, kc, bt[:1], sl)
+    with pytest.raises(ValueError, match="GPU"):
+        fa.tilelang_decode_forward(q, kc, kc, bt, sl)
+
+
+def test_public_api_matches_reference_signatures():
+    import inspect
+    sig = inspect.signature(fa.tilelang_flash_attn_func)
+    assert list(sig.parameters) == ["q", "k", "v", "dropout_p", "softmax_scale", "causal",
+                                    "window_size", "softcap", "alibi_slopes", "deterministic",
+                                    "return_attn_probs"]
+    assert sig.parameters["causal"].default is False
+    sig = inspect.signature(fa.tilelang_paged_forward)
+    assert list(sig.parameters) == ["q", "k_cache", "v_cache", "block_table", "seq_lens",
+                                    "query_start_loc", "prefix_kv_lens", "out", "block_size",
+                                    "num_kv_heads", "softmax_scale", "causal",
+                                    "sliding_window_q", "sliding_window_k"]
+    assert sig.parameters["causal"].default is True
+    assert sig.parameters["block_size"].default == 16
+    sig = inspect.signature(fa.tilelang_decode_forward)
+    assert list(sig.parameters) == ["q", "k_cache", "v_cache", "block_table", "seq_lens",
+                                    "block_size", "num_kv_heads", "softmax_scale"]
+    assert fa.__all__ == ["tilelang_flash_attn_func", "tilelang_flash_attn_gpu",
+                          "tilelang_paged_forward", "tilelang_decode_forward"]

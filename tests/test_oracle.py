@@ -1,0 +1,277 @@
+"""Pins the CPU oracle (oracle/attention_ref.py) without the reference.
+
+Each oracle function is checked against something other than its own
+formula: brute-force golden vectors (tests/golden/make_golden.py), closed
+forms, invariances, fp64 autograd / finite differences, and bit-exact
+enumeration for the integer parts.  Planted-mistake tests show that a wrong
+mask anchor, a transposed GQA map or a dropped scale would fail them.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_ref as ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def t64(x):
+    return torch.from_numpy(np.asarray(x)).to(torch.float64)
+
+
+# ------------------------------------------------------------------ golden
+
+@pytest.mark.parametrize("name", ["dense_nc", "dense_c_skgt", "dense_c_sqgt"])
+def test_dense_matches_golden(gold, name):
+    q, k, v = (t64(gold[f"{name}/{x}"]) for x in "qkv")
+    out, lse = ref.dense_attention(q, k, v, float(gold[f"{name}/scale"]),
+                                   bool(gold[f"{name}/causal"]), dtype=torch.float64)
+    torch.testing.assert_close(out, t64(gold[f"{name}/out"]), atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(lse, t64(gold[f"{name}/lse"]), atol=1e-12, rtol=1e-12)
+
+
+def test_dense_empty_rows_are_zero_and_neg_inf(gold):
+    # Sq=6 > Sk=3 causal: rows 0..2 see no key.
+    out, lse = ref.dense_attention(t64(gold["dense_c_sqgt/q"]), t64(gold["dense_c_sqgt/k"]),
+                                   t64(gold["dense_c_sqgt/v"]), 0.5, True, dtype=torch.float64)
+    assert torch.all(out[:, :3] == 0)
+    assert torch.all(torch.isneginf(lse[..., :3]))
+    assert torch.all(torch.isfinite(lse[..., 3:]))
+
+
+def test_backward_matches_finite_differences(gold):
+    q, k, v, do = (t64(gold[f"bwd/{x}"]) for x in ("q", "k", "v", "dout"))
+    dq, dk, dv = ref.dense_attention_backward(q, k, v, do, float(gold["bwd/scale"]), True,
+                                              dtype=torch.float64)
+    for got, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        torch.testing.assert_close(got, t64(gold[f"bwd/{name}"]), atol=1e-7, rtol=1e-6)
+
+
+@pytest.mark.parametrize("tag", ["c", "nc", "win"])
+def test_paged_matches_golden(gold, tag):
+    g = {k.split("/", 1)[1]: v for k, v in gold.items() if k.startswith("paged/")}
+    out, lse = ref.paged_attention(
+        t64(g["q"]), t64(g["k_cache"]), t64(g["v_cache"]), torch.from_numpy(g["block_table"]),
+        g["seq_lens"], g["query_start_loc"], g["prefix_kv_lens"], float(g["scale"]),
+        causal=bool(gold[f"paged_{tag}/causal"]), window_q=int(gold[f"paged_{tag}/wq"]),
+        window_k=int(gold[f"paged_{tag}/wk"]), dtype=torch.float64)
+    torch.testing.assert_close(out, t64(gold[f"paged_{tag}/out"]), atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(lse, t64(gold[f"paged_{tag}/lse"]), atol=1e-12, rtol=1e-12)
+
+
+def test_decode_matches_golden(gold):
+    g = {k.split("/", 1)[1]: v for k, v in gold.items() if k.startswith("decode/")}
+    out, lse = ref.decode_attention(t64(g["q"]), t64(g["k_cache"]), t64(g["v_cache"]),
+                                    torch.from_numpy(g["block_table"]), g["seq_lens"],
+                                    float(g["scale"]), dtype=torch.float64)
+    torch.testing.assert_close(out, t64(g["out"]), atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(lse, t64(g["lse"]), atol=1e-12, rtol=1e-12)
+
+
+# ------------------------------------------------------------------ closed forms
+
+def test_zero_query_gives_mean_of_visible_values():
+    g = torch.Generator().manual_seed(1)
+    k = torch.randn(1, 9, 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(1, 9, 2, 8, generator=g, dtype=torch.float64)
+    q = torch.zeros(1, 6, 2, 8, dtype=torch.float64)
+    out, lse = ref.dense_attention(q, k, v, 0.3, causal=True, dtype=torch.float64)
+    for i in range(6):
+        n = i + 9 - 6 + 1  # visible keys of row i
+        torch.testing.assert_close(out[0, i], v[0, :n].mean(0), atol=1e-12, rtol=0)
+        torch.testing.assert_close(lse[0, :, i], torch.full((2,), math.log(n), dtype=torch.float64),
+                                   atol=1e-12, rtol=0)
+
+
+def test_single_visible_key_returns_that_value_row():
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(1, 4, 1, 16, generator=g)
+    k = torch.randn(1, 4, 1, 16, generator=g)
+    v = torch.randn(1, 4, 1, 16, generator=g)
+    out, lse = ref.dense_attention(q, k, v, 0.25, causal=True)
+    # causal Sq == Sk: row 0 sees only key 0 -> out is exactly v[0], lse = scale * q.k
+    assert torch.equal(out[0, 0, 0], v[0, 0, 0])
+    torch.testing.assert_close(lse[0, 0, 0], 0.25 * (q[0, 0, 0] @ k[0, 0, 0]), atol=1e-6, rtol=0)
+
+
+def test_invariances():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 5, 4, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(2, 11, 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(2, 11, 2, 8, generator=g, dtype=torch.float64)
+    out, lse = ref.dense_attention(q, k, v, 0.4, causal=False, dtype=torch.float64)
+    perm = torch.randperm(11, generator=g)
+    out_p, lse_p = ref.dense_attention(q, k[:, perm], v[:, perm], 0.4, False, dtype=torch.float64)
+    torch.testing.assert_close(out_p, out, atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(lse_p, lse, atol=1e-12, rtol=1e-12)
+    out_s, _ = ref.dense_attention(q, k, 3.0 * v, 0.4, False, dtype=torch.float64)
+    torch.testing.assert_close(out_s, 3.0 * out, atol=1e-12, rtol=1e-12)
+    # GQA equals MHA with explicitly repeated KV heads
+    out_r, _ = ref.dense_attention(q, k.repeat_interleave(2, 2), v.repeat_interleave(2, 2), 0.4,
+                                   False, dtype=torch.float64)
+    torch.testing.assert_close(out_r, out, atol=0, rtol=0)
+
+
+def test_backward_matches_autograd_fp64():
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(2, 7, 4, 8, generator=g, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(2, 9, 2, 8, generator=g, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(2, 9, 2, 8, generator=g, dtype=torch.float64, requires_grad=True)
+    do = torch.randn(2, 7, 4, 8, generator=g, dtype=torch.float64)
+    for causal in (False, True):
+        out, _ = ref.dense_attention(q, k, v, 0.35, causal, dtype=torch.float64)
+        gq, gk, gv = torch.autograd.grad(out, (q, k, v), do)
+        dq, dk, dv = ref.dense_attention_backward(q.detach(), k.detach(), v.detach(), do, 0.35,
+                                                  causal, dtype=torch.float64)
+        torch.testing.assert_close(dq, gq, atol=1e-10, rtol=1e-9)
+        torch.testing.assert_close(dk, gk, atol=1e-10, rtol=1e-9)
+        torch.testing.assert_close(dv, gv, atol=1e-10, rtol=1e-9)
+
+
+# ------------------------------------------------------------------ integer parts (bit-exact)
+
+def test_paged_rows_resolve_every_slot():
+    g = torch.Generator().manual_seed(5)
+    for page in (1, 4, 16):
+        pool = 13
+        cache = torch.randn(pool, page, 3, 8, generator=g)
+        perm = torch.randperm(pool, generator=g).to(torch.int32)
+        n = min(pool * page, 5 * page + page // 2 + 1)
+        rows = ref.paged_rows(cache, perm, n)
+        for pos in range(n):
+            assert torch.equal(rows[pos], cache[int(perm[pos // page]), pos % page])
+
+
+def test_paged_visible_matches_enumeration():
+    rng = np.random.default_rng(6)
+    for _ in range(40):
+        ql = int(rng.integers(0, 9))
+        pf = int(rng.integers(0, 12))
+        sl = pf + ql + int(rng.integers(-2, 3))
+        sl = max(sl, 0)
+        causal = bool(rng.integers(0, 2))
+        wq = int(rng.integers(-1, 5))
+        wk = int(rng.integers(-1, 5))
+        vis = ref.paged_visible(ql, sl, pf, causal, wq, wk)
+        for t in range(ql):
+            for n in range(sl):
+                exp = (n <= pf + t) if causal else True
+                if causal and wq > 0:
+                    exp = exp and (t < n + wq)
+                if causal and wk > 0:
+                    exp = exp and (n < t + wk)
+                assert bool(vis[t, n]) == exp
+
+
+def test_paged_prefill_equals_dense_causal_when_prefix_is_history():
+    # seq_len = prefix + q_len makes the prefix-anchored mask bottom-right
+    # aligned, i.e. the dense causal convention (tests/test_gqa_paged.py:150-219).
+    g = torch.Generator().manual_seed(7)
+    page, Hq, Hkv, D = 4, 6, 2, 8
+    q_len, total = 5, 13
+    k = torch.randn(1, total, Hkv, D, generator=g)
+    v = torch.randn(1, total, Hkv, D, generator=g)
+    q = torch.randn(1, q_len, Hq, D, generator=g)
+    npg = -(-total // page)
+    perm = torch.randperm(npg + 3, generator=g)
+    kc = torch.full((npg + 3, page, Hkv, D), float("nan"))
+    vc = kc.clone()
+    for pos in range(total):
+        kc[perm[pos // page], pos % page] = k[0, pos]
+        vc[perm[pos // page], pos % page] = v[0, pos]
+    bt = perm[:npg].to(torch.int32).unsqueeze(0)
+    out, lse = ref.paged_attention(q[0], kc, vc, bt, [total], [0, q_len], [total - q_len],
+                                   0.3, causal=True)
+    d_out, d_lse = ref.dense_attention(q, k, v, 0.3, causal=True)
+    torch.testing.assert_close(out, d_out[0], atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(lse, d_lse[0], atol=1e-6, rtol=1e-6)
+
+
+def test_decode_equals_paged_single_token():
+    g = torch.Generator().manual_seed(8)
+    kc = torch.randn(9, 4, 2, 8, generator=g)
+    vc = torch.randn(9, 4, 2, 8, generator=g)
+    bt = torch.randperm(9, generator=g).to(torch.int32).view(3, 3)
+    seq = [3, 12, 7]
+    q = torch.randn(3, 4, 8, generator=g)
+    out, lse = ref.decode_attention(q, kc, vc, bt, seq, 0.5)
+    for b in range(3):
+        o, l = ref.paged_attention(q[b:b + 1], kc, vc, bt[b:b + 1], [seq[b]], [0, 1],
+                                   [seq[b] - 1], 0.5, causal=True)
+        torch.testing.assert_close(out[b], o[0], atol=1e-6, rtol=1e-6)
+        torch.testing.assert_close(lse[b], l[:, 0], atol=1e-6, rtol=1e-6)
+
+
+def test_merge_of_split_partials_equals_unsplit():
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(1, 1, 3, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 50, 3, 16, generator=g, dtype=torch.float64)
+    v = torch.randn(1, 50, 3, 16, generator=g, dtype=torch.float64)
+    full_o, full_l = ref.dense_attention(q, k, v, 0.25, False, dtype=torch.float64)
+    cuts = [0, 7, 8, 31, 50]
+    outs, lses = [], []
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        o, l = ref.dense_attention(q, k[:, a:b], v[:, a:b], 0.25, False, dtype=torch.float64)
+        outs.append(o)
+        lses.append(l.transpose(1, 2))  # [B, Sq, H]
+    mo, ml = ref.merge_partials(torch.stack(outs), torch.stack(lses))
+    torch.testing.assert_close(mo, full_o, atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(ml, full_l.transpose(1, 2), atol=1e-12, rtol=1e-12)
+    # an empty partial (lse = -inf) does not change the merge
+    mo2, _ = ref.merge_partials(torch.cat([torch.stack(outs), torch.zeros_like(outs[0])[None]]),
+                                torch.cat([torch.stack(lses), torch.full_like(lses[0], -math.inf)[None]]))
+    torch.testing.assert_close(mo2, full_o, atol=1e-12, rtol=1e-12)
+
+
+def test_pair_counts_match_enumeration_and_survey_configs():
+    for sq, sk, c in ((5, 7, True), (7, 5, True), (6, 6, False), (2048, 2048, True)):
+        assert ref.dense_pairs(sq, sk, c) == int(ref.dense_visible(sq, sk, c).sum())
+    assert ref.dense_pairs(2048, 2048, True) == 2_098_176
+    lens = [2641, 2501, 1405, 3002, 2670, 3056, 3789, 615]
+    assert ref.paged_pairs(lens, lens, [0] * 8) == 27_719_186
+    pf = [1751, 3120, 3566, 3048, 244, 5664, 6907, 5746, 127, 492, 1652, 980, 5907, 6417, 6694, 2486]
+    assert ref.paged_pairs([512] * 16, [p + 512 for p in pf], pf) == 30_159_360
+
+
+# ------------------------------------------------------------------ planted mistakes
+
+def test_planted_top_left_causal_mask_is_caught(gold, monkeypatch):
+    def top_left(sq, sk, causal):
+        i = torch.arange(sq).unsqueeze(1)
+        j = torch.arange(sk).unsqueeze(0)
+        return j <= i if causal else torch.ones(sq, sk, dtype=torch.bool)
+
+    monkeypatch.setattr(ref, "dense_visible", top_left)
+    with pytest.raises(AssertionError):
+        test_dense_matches_golden(gold, "dense_c_skgt")
+
+
+def test_planted_transposed_gqa_map_is_caught(gold, monkeypatch):
+    def wrong_expand(k, heads):
+        g = heads // k.shape[2]
+        return k.repeat(1, 1, g, 1)  # head h -> kv head h % Hk (wrong)
+
+    monkeypatch.setattr(ref, "_expand_kv", wrong_expand)
+    with pytest.raises(AssertionError):
+        test_paged_matches_golden(gold, "c")
+
+
+def test_planted_dropped_scale_in_dk_is_caught(gold, monkeypatch):
+    orig = ref.dense_attention_backward
+
+    def no_scale_dk(*a, **kw):
+        dq, dk, dv = orig(*a, **kw)
+        return dq, dk / float(gold["bwd/scale"]), dv
+
+    monkeypatch.setattr(ref, "dense_attention_backward", no_scale_dk)
+    with pytest.raises(AssertionError):
+        test_backward_matches_finite_differences(gold)

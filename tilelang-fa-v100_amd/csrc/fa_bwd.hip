@@ -1,0 +1,448 @@
+// Dense attention backward for gfx950 (FlashAttention-2, LSE recompute).
+//
+// Replaces tilelang_backward (tilelang_fa_v100/_kernels_backward.py:200-208):
+// the PyTorch row_dot (:203), the dQ kernel (:10-85) and the dK/dV kernel
+// (:88-176).  The reference recomputes QK^T and dO V^T in both kernels (7
+// GEMMs per tile pair); here one KV-stationary kernel does the 5 GEMMs
+//   S = Q K^T,  dP = dO V^T,  dV += P^T dO,  dK += dS^T Q,  dQ += dS K
+// with P = exp(scale*S - lse), dS = P * (dP - rowdot(O, dO))
+// (_kernels_backward.py:72-74,159-170).  dQ is reduced across KV tiles with
+// fp32 atomics into a caller-provided workspace and converted afterwards.
+//
+// Kernels:
+//   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row; zeroes
+//                       the dQ accumulator rows it covers.
+//   bwd_main_kernel     workgroup = 128 keys (32 per wave) of one KV head;
+//                       loops over the 64-row query tiles of every query
+//                       head that shares the KV head (GQA).  K and V of the wave stay in registers,
+//                       K^T of the workgroup stays in LDS.
+//   bwd_dq_convert      dQ = scale * acc, cast to the input dtype.
+#include "fa_common.h"
+#include "fa_internal.h"
+
+namespace fa {
+
+template <int D>
+struct BwdShape {
+  static constexpr int BKV = 128;         // keys per workgroup
+  static constexpr int BQ = 64;           // query rows per iteration
+  static constexpr int NQT = BQ / 32;     // 32-row query sub-tiles
+  static constexpr int DC = D / 16;       // 16-wide d chunks (QK^T, dO V^T)
+  static constexpr int DT = D / 32;       // 32-wide d tiles (dK^T, dV^T, dQ)
+  static constexpr int CPR = D / 8;       // 16-byte chunks per row
+  static constexpr int RG = BQ * CPR / 256;  // consecutive rows per thread
+  static constexpr int QS = D + 8;        // natural Q / dO row stride
+  static constexpr int TS = BQ + 4;       // transposed Q / dO row stride
+  static constexpr int SS = BKV + 8;      // dS row stride
+  static constexpr int KTS = BKV + 8;     // K^T row stride
+  static constexpr int OFF_QS = 0;
+  static constexpr int OFF_DOS = OFF_QS + BQ * QS;
+  static constexpr int OFF_QT = OFF_DOS + BQ * QS;
+  static constexpr int OFF_DOT = OFF_QT + D * TS;
+  static constexpr int OFF_DS = OFF_DOT + D * TS;
+  static constexpr int OFF_KT = OFF_DS + BQ * SS;
+  static constexpr int LDS_ELEMS = OFF_KT + D * KTS;
+  static_assert(RG == 2 || RG == 4, "row grouping");
+};
+
+// ------------------------------------------------------------ preprocess
+template <class T, int D>
+__global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqacc,
+                                                      float* rowdot, float* lse2) {
+  constexpr int LPR = D / 8;          // lanes per row
+  constexpr int RPB = 256 / LPR;      // rows per block
+  const int64_t nrows = (int64_t)a.batch * a.seqlen_q * a.num_heads;
+  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  float acc = 0.f;
+  int b = 0, q = 0, h = 0;
+  if (r < nrows) {
+    h = (int)(r % a.num_heads);
+    const int64_t bq = r / a.num_heads;
+    q = (int)(bq % a.seqlen_q);
+    b = (int)(bq / a.seqlen_q);
+    const uint16_t* op = static_cast<const uint16_t*>(a.out) + b * a.o_stride[0] +
+                         q * a.o_stride[1] + h * a.o_stride[2] + 8 * sub;
+    const uint16_t* dp = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
+                         q * a.do_stride[1] + h * a.do_stride[2] + 8 * sub;
+    const u32x4 ov = ld16(op), dv = ld16(dp);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      acc += T::lo(ov[w]) * T::lo(dv[w]) + T::hi(ov[w]) * T::hi(dv[w]);
+    float* z = dqacc + r * D + 8 * sub;
+    st16(z, u32x4{0, 0, 0, 0});
+    st16(z + 4, u32x4{0, 0, 0, 0});
+  }
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if (r < nrows && sub == 0) {
+    const int64_t idx = ((int64_t)b * a.num_heads + h) * a.seqlen_q + q;
+    rowdot[idx] = acc;
+    const float l = a.lse[idx];
+    // A row that saw no key has lse = -inf; +inf makes its P exactly zero.
+    lse2[idx] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
+  }
+}
+
+// ------------------------------------------------------------ main kernel
+template <class T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqacc,
+                                                       const float* rowdot,
+                                                       const float* lse2) {
+  using S = BwdShape<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
+  __shared__ __attribute__((aligned(16))) float lse_s[S::BQ];
+  __shared__ __attribute__((aligned(16))) float di_s[S::BQ];
+  uint16_t* Qs = smem + S::OFF_QS;
+  uint16_t* dOs = smem + S::OFF_DOS;
+  uint16_t* Qt = smem + S::OFF_QT;
+  uint16_t* dOt = smem + S::OFF_DOT;
+  uint16_t* dSs = smem + S::OFF_DS;
+  uint16_t* Kt = smem + S::OFF_KT;
+
+  const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads, Hk = a.num_heads_k;
+  const int G = H / Hk;  // query heads sharing this KV head
+  const int kvtiles = (Sk + S::BKV - 1) / S::BKV;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt_idx = id % kvtiles;  // smallest key index first: most query rows
+  const int bh = id / kvtiles;
+  const int hk = bh % Hk, b = bh / Hk;
+  const int kv0 = kt_idx * S::BKV;
+  const int off = Sk - Sq;  // key n visible to query i iff n <= i + off
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int kv0w = kv0 + 32 * wave;
+  const int my_kv = kv0w + lr;
+  const float scale_log2 = a.softmax_scale * kLog2e;
+
+  const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
+  const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
+
+  // ---- stationary operands: K, V rows of this lane (B operands), K^T in LDS.
+  u32x4 kB[S::DC], vB[S::DC];
+  {
+    const bool ok = my_kv < Sk;
+    const uint16_t* kp = kg + (int64_t)my_kv * a.k_stride[1];
+    const uint16_t* vp = vg + (int64_t)my_kv * a.v_stride[1];
+#pragma unroll
+    for (int c = 0; c < S::DC; ++c) {
+      kB[c] = ok ? ld16(kp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
+      vB[c] = ok ? ld16(vp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
+    }
+    const int col8 = tid % S::CPR, grp = tid / S::CPR;
+    constexpr int GPP = 256 / S::CPR;  // 4-row groups per pass
+#pragma unroll
+    for (int p = 0; p < S::BKV / (4 * GPP); ++p) {
+      const int rbase = 4 * (grp + GPP * p);
+      u32x4 rows[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = kv0 + rbase + r;
+        rows[r] = n < Sk ? ld16(kg + (int64_t)n * a.k_stride[1] + 8 * col8)
+                         : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int w = j >> 1;
+        u32x2 pr;
+        pr[0] = (j & 1) ? pack_hi(rows[0][w], rows[1][w]) : pack_lo(rows[0][w], rows[1][w]);
+        pr[1] = (j & 1) ? pack_hi(rows[2][w], rows[3][w]) : pack_lo(rows[2][w], rows[3][w]);
+        st8(Kt + (8 * col8 + j) * S::KTS + rbase, pr);
+      }
+    }
+  }
+
+  f32x16 dk[S::DT], dv[S::DT];
+#pragma unroll
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
+
+  // Query rows that can see any key of this tile.
+  const int q_begin = CAUSAL ? max(0, kv0 - off) : 0;
+  const int it0 = q_begin / S::BQ;
+  const int it1 = (Sq + S::BQ - 1) / S::BQ;
+  const int nit = max(it1 - it0, 0);
+  const int wkv_last = min(kv0w + 31, Sk - 1);
+
+  // Iteration t covers query head hk*G + t / nit, query tile it0 + t % nit.
+  // Q / dO tile loader: thread owns column chunk col8 of RG consecutive rows.
+  const int col8 = tid % S::CPR;
+  const int rg0 = (tid / S::CPR) * S::RG;
+  u32x4 qreg[S::RG], doreg[S::RG];
+  float lreg = 0.f, dreg = 0.f;
+  auto load_q = [&](int t) {
+    const int h = hk * G + t / nit;
+    const int i0 = (it0 + t % nit) * S::BQ;
+    const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] + h * a.q_stride[2];
+    const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
+                          h * a.do_stride[2];
+    const int64_t stat0 = ((int64_t)b * H + h) * Sq;
+#pragma unroll
+    for (int r = 0; r < S::RG; ++r) {
+      const int i = i0 + rg0 + r;
+      const bool ok = i < Sq;
+      qreg[r] = ok ? ld16(qg + (int64_t)i * a.q_stride[1] + 8 * col8) : u32x4{0, 0, 0, 0};
+      doreg[r] = ok ? ld16(dog + (int64_t)i * a.do_stride[1] + 8 * col8) : u32x4{0, 0, 0, 0};
+    }
+    if (tid < S::BQ) {
+      const int i = i0 + tid;
+      lreg = i < Sq ? lse2[stat0 + i] : __builtin_inff();
+      dreg = i < Sq ? rowdot[stat0 + i] : 0.f;
+    }
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int r = 0; r < S::RG; ++r) {
+      st16(Qs + (rg0 + r) * S::QS + 8 * col8, qreg[r]);
+      st16(dOs + (rg0 + r) * S::QS + 8 * col8, doreg[r]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int w = j >> 1;
+      if constexpr (S::RG == 4) {
+        u32x2 pq, pd;
+        pq[0] = (j & 1) ? pack_hi(qreg[0][w], qreg[1][w]) : pack_lo(qreg[0][w], qreg[1][w]);
+        pq[1] = (j & 1) ? pack_hi(qreg[2][w], qreg[3][w]) : pack_lo(qreg[2][w], qreg[3][w]);
+        pd[0] = (j & 1) ? pack_hi(doreg[0][w], doreg[1][w]) : pack_lo(doreg[0][w], doreg[1][w]);
+        pd[1] = (j & 1) ? pack_hi(doreg[2][w], doreg[3][w]) : pack_lo(doreg[2][w], doreg[3][w]);
+        st8(Qt + (8 * col8 + j) * S::TS + rg0, pq);
+        st8(dOt + (8 * col8 + j) * S::TS + rg0, pd);
+      } else {
+        const uint32_t pq = (j & 1) ? pack_hi(qreg[0][w], qreg[1][w]) : pack_lo(qreg[0][w], qreg[1][w]);
+        const uint32_t pd = (j & 1) ? pack_hi(doreg[0][w], doreg[1][w]) : pack_lo(doreg[0][w], doreg[1][w]);
+        *reinterpret_cast<uint32_t*>(Qt + (8 * col8 + j) * S::TS + rg0) = pq;
+        *reinterpret_cast<uint32_t*>(dOt + (8 * col8 + j) * S::TS + rg0) = pd;
+      }
+    }
+    if (tid < S::BQ) {
+      lse_s[tid] = lreg;
+      di_s[tid] = dreg;
+    }
+  };
+
+  const int ntot = nit * G;
+  if (ntot > 0) {
+    load_q(0);
+    store_q();
+  }
+  for (int t = 0; t < ntot; ++t) {
+    const int h = hk * G + t / nit;
+    const int i0 = (it0 + t % nit) * S::BQ;
+    __syncthreads();  // Q/dO tile (and K^T on the first pass) visible
+    const bool more = t + 1 < ntot;
+    if (more) load_q(t + 1);
+
+    // Does this wave's key block see any of these query rows?
+    const bool active = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0w);
+    const bool wvalid = kv0w < Sk;
+    if (active && wvalid) {
+      f32x16 s[S::NQT], dp[S::NQT];
+#pragma unroll
+      for (int qt = 0; qt < S::NQT; ++qt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[qt][i] = dp[qt][i] = 0.f;
+#pragma unroll
+        for (int c = 0; c < S::DC; ++c) {
+          const u32x4 aq = ld16(Qs + (qt * 32 + lr) * S::QS + 16 * c + 8 * lh);
+          const u32x4 ado = ld16(dOs + (qt * 32 + lr) * S::QS + 16 * c + 8 * lh);
+          s[qt] = T::mma32(aq, kB[c], s[qt]);
+          dp[qt] = T::mma32(ado, vB[c], dp[qt]);
+        }
+      }
+      // Masking is needed on the diagonal band and on a partial key block.
+      const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kv0w + 32 > Sk);
+#pragma unroll
+      for (int qt = 0; qt < S::NQT; ++qt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int qb = qt * 32 + 8 * g + 4 * lh;  // first of 4 rows
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse_s + qb);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(di_s + qb);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = 4 * g + r;
+            float p = fast_exp2(fmaf(s[qt][i], scale_log2, -l4[r]));
+            if (need_mask) {
+              const int qi = i0 + qb + r;
+              const bool vis = (my_kv < Sk) && (!CAUSAL || my_kv <= qi + off);
+              p = vis ? p : 0.f;
+            }
+            s[qt][i] = p;                       // P
+            dp[qt][i] = p * (dp[qt][i] - d4[r]);  // dS (unscaled)
+          }
+        }
+      // Pack P and dS as B operands; write dS to LDS for the dQ product.
+      u32x4 pB[2 * S::NQT], sB[2 * S::NQT];
+#pragma unroll
+      for (int kq = 0; kq < 2 * S::NQT; ++kq)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int e = 8 * (kq & 1) + 2 * w;
+          pB[kq][w] = T::pack(s[kq >> 1][e], s[kq >> 1][e + 1]);
+          sB[kq][w] = T::pack(dp[kq >> 1][e], dp[kq >> 1][e + 1]);
+        }
+#pragma unroll
+      for (int kq = 0; kq < 2 * S::NQT; ++kq)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          // halves of sB[kq][w] are entries e, e+1 = rows qrow, qrow+1
+          const int e = 8 * (kq & 1) + 2 * w;
+          const int qrow = (kq >> 1) * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
+          const uint32_t v = sB[kq][w];
+          dSs[qrow * S::SS + 32 * wave + lr] = (uint16_t)(v & 0xffffu);
+          dSs[(qrow + 1) * S::SS + 32 * wave + lr] = (uint16_t)(v >> 16);
+        }
+      // dV^T += dO^T P,  dK^T += Q^T dS
+#pragma unroll
+      for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+        for (int kq = 0; kq < 2 * S::NQT; ++kq) {
+          const int qo = 16 * kq + 4 * lh;
+          const uint16_t* tq = Qt + (dt * 32 + lr) * S::TS + qo;
+          const uint16_t* td = dOt + (dt * 32 + lr) * S::TS + qo;
+          const u32x2 q0 = ld8(tq), q1 = ld8(tq + 8);
+          const u32x2 d0 = ld8(td), d1 = ld8(td + 8);
+          const u32x4 aq = {q0[0], q0[1], q1[0], q1[1]};
+          const u32x4 ad = {d0[0], d0[1], d1[0], d1[1]};
+          dv[dt] = T::mma32(ad, pB[kq], dv[dt]);
+          dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
+        }
+    } else {
+      // Inactive waves contribute zero dS to the shared dQ product.
+#pragma unroll
+      for (int q = 0; q < S::BQ; ++q) dSs[q * S::SS + 32 * wave + lr] = 0;
+    }
+    __syncthreads();  // dS complete; Q/dO tiles no longer read
+    if (more) store_q();
+
+    // dQ[i0 + q][d] += sum_k dS[q][k] K[k][d] over this workgroup's 128 keys.
+    {
+      const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
+      if (any) {
+        float* dqb = dqacc + (((int64_t)b * Sq) * H + h) * D;
+        const int64_t qstride = (int64_t)H * D;
+#pragma unroll
+        for (int pr = wave; pr < S::NQT * S::DT; pr += 4) {
+          const int qt = pr % S::NQT, dt = pr / S::NQT;
+          f32x16 acc;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+          for (int kc = 0; kc < S::BKV / 16; ++kc) {
+            const u32x4 as = ld16(dSs + (qt * 32 + lr) * S::SS + 16 * kc + 8 * lh);
+            const u32x4 bk = ld16(Kt + (dt * 32 + lr) * S::KTS + 16 * kc + 8 * lh);
+            acc = T::mma32(as, bk, acc);
+          }
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int qi = i0 + qt * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+            if (qi < Sq) unsafeAtomicAdd(dqb + qi * qstride + dt * 32 + lr, acc[i]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: this lane's key row.
+  if (my_kv < Sk) {
+    uint16_t* dkp = static_cast<uint16_t*>(a.dk) + b * a.dk_stride[0] +
+                    (int64_t)my_kv * a.dk_stride[1] + hk * a.dk_stride[2];
+    uint16_t* dvp = static_cast<uint16_t*>(a.dv) + b * a.dv_stride[0] +
+                    (int64_t)my_kv * a.dv_stride[1] + hk * a.dv_stride[2];
+    const float sc = a.softmax_scale;
+#pragma unroll
+    for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * dt + 8 * g + 4 * lh;
+        u32x2 wk, wv;
+        wk[0] = T::pack(dk[dt][4 * g] * sc, dk[dt][4 * g + 1] * sc);
+        wk[1] = T::pack(dk[dt][4 * g + 2] * sc, dk[dt][4 * g + 3] * sc);
+        wv[0] = T::pack(dv[dt][4 * g], dv[dt][4 * g + 1]);
+        wv[1] = T::pack(dv[dt][4 * g + 2], dv[dt][4 * g + 3]);
+        st8(dkp + d, wk);
+        st8(dvp + d, wv);
+      }
+  }
+}
+
+// ------------------------------------------------------------ dQ convert
+template <class T, int D>
+__global__ __launch_bounds__(256) void bwd_dq_convert_kernel(fa_bwd_args a,
+                                                             const float* dqacc) {
+  constexpr int LPR = D / 8;
+  constexpr int RPB = 256 / LPR;
+  const int64_t nrows = (int64_t)a.batch * a.seqlen_q * a.num_heads;
+  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  if (r >= nrows) return;
+  const int h = (int)(r % a.num_heads);
+  const int64_t bq = r / a.num_heads;
+  const int q = (int)(bq % a.seqlen_q);
+  const int b = (int)(bq / a.seqlen_q);
+  const float* src = dqacc + r * D + 8 * sub;
+  const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
+  const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
+  const float sc = a.softmax_scale;
+  u32x4 w;
+  w[0] = T::pack(x0[0] * sc, x0[1] * sc);
+  w[1] = T::pack(x0[2] * sc, x0[3] * sc);
+  w[2] = T::pack(x1[0] * sc, x1[1] * sc);
+  w[3] = T::pack(x1[2] * sc, x1[3] * sc);
+  uint16_t* dst = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] + q * a.dq_stride[1] +
+                  h * a.dq_stride[2] + 8 * sub;
+  st16(dst, w);
+}
+
+// ----------------------------------------------------------------- launchers
+
+size_t bwd_workspace_bytes(const fa_bwd_args& a) {
+  const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
+  return rows * a.head_dim * sizeof(float) + 2 * rows * sizeof(float) + 256;
+}
+
+template <class T, int D>
+static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
+  using S = BwdShape<D>;
+  const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
+  float* dqacc = static_cast<float*>(ws);
+  float* rowdot = dqacc + rows * D;
+  float* lse2 = rowdot + rows;
+  constexpr int RPB = 256 / (D / 8);
+  const dim3 rgrid((unsigned)((rows + RPB - 1) / RPB));
+  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, rowdot, lse2);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
+  const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
+  if (kvtiles == 0) {
+    // No keys: dQ stays zero; dK / dV are empty.
+  } else if (a.causal)
+    hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc,
+                       rowdot, lse2);
+  else
+    hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc,
+                       rowdot, lse2);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((bwd_dq_convert_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc);
+  return hipGetLastError();
+}
+
+template <class T>
+static hipError_t launch_bwd_t(const fa_bwd_args& a, void* ws, hipStream_t st) {
+  switch (a.head_dim) {
+    case 64: return launch_bwd_d<T, 64>(a, ws, st);
+    case 128: return launch_bwd_d<T, 128>(a, ws, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd(const fa_bwd_args& a, void* ws, hipStream_t st) {
+  return a.dtype == FA_DTYPE_BF16 ? launch_bwd_t<BFloat16>(a, ws, st)
+                                  : launch_bwd_t<Half>(a, ws, st);
+}
+
+}  // namespace fa

@@ -1,0 +1,129 @@
+// Shared device-side definitions for the gfx950 attention kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * A wavefront has 64 lanes.  `lane & 31` is written `lr` and `lane >> 5`
+//    is written `lh`.
+//  * The 32x32x16 MFMA (v_mfma_f32_32x32x16_{f16,bf16}) takes, per lane, an
+//    8-element A vector holding A[row = lr][k = 8*lh + j] and an 8-element B
+//    vector holding B[k = 8*lh + j][col = lr]; the 16 accumulators of a lane
+//    hold C[row = 8*(i/4) + 4*lh + (i%4)][col = lr].
+//    Because the hardware pairs A element (lane, j) with B element (lane, j),
+//    any bijection from (lh, j) to the 16 k indices may be used as long as A
+//    and B use the same one.  The kernels use that freedom so that the
+//    accumulator of one product can be fed, without data movement, as the B
+//    operand of the next one.
+//  * 16-bit data are moved as raw 32-bit words (two elements per word, the
+//    lower-indexed element in the low half).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+// Element-type traits.  `Half` is IEEE binary16, `BFloat16` is bfloat16.
+struct Half {
+  static constexpr int kId = 0;
+  __device__ __forceinline__ static f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f32x4 mma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // Round-to-nearest-even conversion of two floats into one packed word.
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
+    f16x2 v;
+    v[0] = (_Float16)lo;
+    v[1] = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, w)[0];
+  }
+  __device__ __forceinline__ static float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, w)[1];
+  }
+};
+
+struct BFloat16 {
+  static constexpr int kId = 1;
+  __device__ __forceinline__ static f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f32x4 mma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
+    bf16x2 v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) {
+    return __builtin_bit_cast(float, w << 16);
+  }
+  __device__ __forceinline__ static float hi(uint32_t w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+};
+
+// Low 16 bits of `a` and of `b` packed as {a.lo, b.lo}; likewise for the high
+// halves.  Used to transpose 16-bit matrices held in registers.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+// Exchange with the lane 32 positions away (lane ^ 32).
+__device__ __forceinline__ float swap_halves(float x) {
+  return __shfl_xor(x, 32);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+__device__ __forceinline__ u32x2 ld8(const void* p) {
+  return *reinterpret_cast<const u32x2*>(p);
+}
+__device__ __forceinline__ void st8(void* p, u32x2 v) {
+  *reinterpret_cast<u32x2*>(p) = v;
+}
+
+// XCD-aware workgroup order.  The hardware hands consecutive workgroup ids to
+// the 8 XCDs round-robin; remapping makes each XCD receive a contiguous range
+// of logical tiles, so tiles that share K/V rows share one L2.
+__device__ __forceinline__ int xcd_remap(int linear, int total) {
+  constexpr int kXcds = 8;
+  if (total % kXcds != 0) return linear;
+  const int per = total / kXcds;
+  return (linear % kXcds) * per + linear / kXcds;
+}
+
+}  // namespace fa

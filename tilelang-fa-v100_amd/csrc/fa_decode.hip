@@ -1,0 +1,306 @@
+// Paged decode for gfx950: split-KV partials + LSE-merge combine.
+//
+// Replaces _decode_kernel_func (tilelang_fa_v100/_kernels_paged.py:393-489),
+// which runs one workgroup per (query head, sequence), walks the whole
+// context serially and re-reads every KV head once per query head.  Here a
+// workgroup owns (fixed-size key chunk, KV head, head group, sequence):
+//   * all GB query heads of a GQA group are served by one read of the chunk's
+//     K and V rows (GB = largest of 8/4/2/1 dividing Hq/Hkv);
+//   * phase 1: S^T = K Q^T on the 16x16x32 MFMA (A = K rows straight from
+//     the paged cache, 16-byte loads; B = Q^T, unused head columns zero);
+//   * phase 2: per-head max / exp2 / sum over the chunk in LDS;
+//   * phase 3: O += P V on the VALU, each lane owning 8 contiguous d of a V
+//     row, followed by a cross-lane and cross-wave reduction;
+//   * each chunk writes a normalised partial O (fp32) and its base-2 LSE; the
+//     combine kernel merges chunks with LSE weights (the online-softmax merge
+//     of the dormant split variant, _kernels_paged.py:175-187).
+// The decode mask is `key < seq_len` (_kernels_paged.py:450-451).
+#include "fa_common.h"
+#include "fa_internal.h"
+
+namespace fa {
+
+constexpr int kDecChunk = 256;  // keys per split workgroup
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+struct DecodeWs {
+  float* po;    // [B, Hq, nsplit, D]   normalised partial outputs
+  float* plse;  // [B, Hq, nsplit]      base-2 log-sum-exp of each chunk
+  int nsplit;
+};
+
+template <class T, int D, int GB>
+__global__ __launch_bounds__(256) void decode_split_kernel(fa_decode_args a,
+                                                           DecodeWs ws) {
+  constexpr int CH = kDecChunk;
+  constexpr int LPT = D / 8;       // lanes per V row in phase 3
+  constexpr int TPW = 64 / LPT;    // rows per wave per pass in phase 3
+  constexpr int TPB = 4 * TPW;     // rows per workgroup per pass
+  constexpr int DC = D / 32;       // 32-wide d chunks of the QK^T MFMA
+  __shared__ float s_lds[GB][CH];
+  __shared__ float red[4][GB][D];
+  __shared__ float stat_m[GB], stat_l[GB];
+
+  const int G = a.num_heads / a.num_kv_heads;
+  const int ngroups = G / GB;
+  const int id = blockIdx.x;
+  const int c = id % ws.nsplit;
+  int rest = id / ws.nsplit;
+  const int hg = rest % ngroups;
+  rest /= ngroups;
+  const int hk = rest % a.num_kv_heads;
+  const int b = rest / a.num_kv_heads;
+
+  const int seq_len = max(0, min(a.seq_lens[b], a.max_blocks * a.page_size));
+  const int n_begin = c * CH;
+  if (n_begin >= seq_len) return;
+  const int n_end = min(n_begin + CH, seq_len);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h0 = hk * G + hg * GB;  // first query head of this group
+  const uint16_t* kc = static_cast<const uint16_t*>(a.k_cache) + (int64_t)hk * a.k_stride[2];
+  const uint16_t* vc = static_cast<const uint16_t*>(a.v_cache) + (int64_t)hk * a.v_stride[2];
+  const int32_t* bt = a.block_table + (int64_t)b * a.block_table_stride;
+  const int ps_log2 = __builtin_ctz(a.page_size);
+  const int ps_mask = a.page_size - 1;
+  const unsigned last_page = (unsigned)(a.num_pages - 1);
+  auto page_of = [&](int n) -> int64_t {
+    return (int64_t)min((unsigned)bt[n >> ps_log2], last_page);
+  };
+  const float scale_log2 = a.softmax_scale * kLog2e;
+
+  // ---- phase 1: scores.  Wave w handles 16-key blocks w, w+4, ...
+  {
+    const int l16 = lane & 15, lq = lane >> 4;
+    u32x4 qb[DC];
+    const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_stride[0] +
+                           (int64_t)(h0 + l16) * a.q_stride[1];
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc)
+      qb[cc] = (l16 < GB) ? ld16(qrow + 32 * cc + 8 * lq) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int it = 0; it < CH / 64; ++it) {
+      const int blk = wave + 4 * it;
+      const int n = n_begin + blk * 16 + l16;
+      u32x4 kr[DC];
+      if (n < n_end) {
+        const uint16_t* kp = kc + page_of(n) * a.k_stride[0] + (n & ps_mask) * a.k_stride[1];
+#pragma unroll
+        for (int cc = 0; cc < DC; ++cc) kr[cc] = ld16(kp + 32 * cc + 8 * lq);
+      } else {
+#pragma unroll
+        for (int cc = 0; cc < DC; ++cc) kr[cc] = u32x4{0, 0, 0, 0};
+      }
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < DC; ++cc) acc = T::mma16(kr[cc], qb[cc], acc);
+      // acc[i] = S^T[key = 4*lq + i][head = l16]
+      if (l16 < GB) {
+        f32x4 sv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int nn = n_begin + blk * 16 + 4 * lq + i;
+          sv[i] = nn < n_end ? acc[i] * scale_log2 : neg_inf();
+        }
+        *reinterpret_cast<f32x4*>(&s_lds[l16][blk * 16 + 4 * lq]) = sv;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: per-head max and sum (base 2).
+  for (int g = wave; g < GB; g += 4) {
+    float m = neg_inf();
+    for (int t = lane; t < CH; t += 64) m = fmaxf(m, s_lds[g][t]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int t = lane; t < CH; t += 64) {
+      const float p = fast_exp2(s_lds[g][t] - m);
+      s_lds[g][t] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      stat_m[g] = m;
+      stat_l[g] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: O = P V.  LPT lanes per key row, 8 d per lane.
+  const int lsub = lane % LPT;
+  const int lrow = lane / LPT;
+  float acc[GB][8];
+#pragma unroll
+  for (int g = 0; g < GB; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
+#pragma unroll
+  for (int t0 = 0; t0 < CH; t0 += TPB) {
+    const int t = t0 + wave * TPW + lrow;
+    const int n = n_begin + t;
+    if (n < n_end) {
+      const uint16_t* vp = vc + page_of(n) * a.v_stride[0] + (n & ps_mask) * a.v_stride[1];
+      const u32x4 vr = ld16(vp + 8 * lsub);
+      float vf[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        vf[2 * w] = T::lo(vr[w]);
+        vf[2 * w + 1] = T::hi(vr[w]);
+      }
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        const float p = s_lds[g][t];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(p, vf[j], acc[g][j]);
+      }
+    }
+  }
+  // Reduce over the key rows held by lanes of equal lsub within the wave.
+#pragma unroll
+  for (int o = LPT; o < 64; o <<= 1)
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] += __shfl_xor(acc[g][j], o);
+  if (lrow == 0) {
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[wave][g][8 * lsub + j] = acc[g][j];
+  }
+  __syncthreads();
+  for (int e = tid; e < GB * D; e += 256) {
+    const int g = e / D, d = e % D;
+    const float sum = red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d];
+    const float l = stat_l[g];
+    const int64_t row = ((int64_t)b * a.num_heads + h0 + g) * ws.nsplit + c;
+    ws.po[row * D + d] = l > 0.f ? sum / l : 0.f;
+    if (d == 0) ws.plse[row] = l > 0.f ? stat_m[g] + log2f(l) : neg_inf();
+  }
+}
+
+// One wave per (sequence, query head): merge the chunk partials.
+template <class T, int D>
+__global__ __launch_bounds__(64) void decode_combine_kernel(fa_decode_args a,
+                                                            DecodeWs ws) {
+  const int hq = blockIdx.x % a.num_heads;
+  const int b = blockIdx.x / a.num_heads;
+  const int lane = threadIdx.x;
+  const int seq_len = max(0, min(a.seq_lens[b], a.max_blocks * a.page_size));
+  const int ns = (seq_len + kDecChunk - 1) / kDecChunk;
+  const int64_t row0 = ((int64_t)b * a.num_heads + hq) * ws.nsplit;
+  float m = neg_inf();
+  for (int c = lane; c < ns; c += 64) m = fmaxf(m, ws.plse[row0 + c]);
+  m = wave_max(m);
+  // Lane owns d pairs 2*lane + 128*k.
+  constexpr int NP = (D + 127) / 128;
+  float acc[NP][2];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) acc[k][0] = acc[k][1] = 0.f;
+  float wsum = 0.f;
+  const float m_use = (m == neg_inf()) ? 0.f : m;
+  for (int c = 0; c < ns; ++c) {
+    const float w = fast_exp2(ws.plse[row0 + c] - m_use);
+    wsum += w;
+    const float* pp = ws.po + (row0 + c) * D;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int d = 2 * lane + 128 * k;
+      if (d < D) {
+        acc[k][0] = fmaf(w, pp[d], acc[k][0]);
+        acc[k][1] = fmaf(w, pp[d + 1], acc[k][1]);
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  uint16_t* op = static_cast<uint16_t*>(a.out) + (int64_t)b * a.o_stride[0] +
+                 (int64_t)hq * a.o_stride[1];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int d = 2 * lane + 128 * k;
+    if (d < D)
+      *reinterpret_cast<uint32_t*>(op + d) = T::pack(acc[k][0] * inv, acc[k][1] * inv);
+  }
+  if (a.lse && lane == 0)
+    a.lse[(int64_t)b * a.num_heads + hq] =
+        wsum > 0.f ? (m_use + log2f(wsum)) * kLn2 : neg_inf();
+}
+
+// ----------------------------------------------------------------- launchers
+
+int decode_num_splits(const fa_decode_args& a) {
+  return (a.max_seq_len + kDecChunk - 1) / kDecChunk;
+}
+
+int decode_group_size(const fa_decode_args& a) {
+  const int G = a.num_heads / a.num_kv_heads;
+  if (G % 8 == 0) return 8;
+  if (G % 4 == 0) return 4;
+  if (G % 2 == 0) return 2;
+  return 1;
+}
+
+size_t decode_workspace_bytes(const fa_decode_args& a) {
+  const size_t rows = (size_t)a.batch * a.num_heads * (size_t)decode_num_splits(a);
+  return rows * (size_t)a.head_dim * sizeof(float) + rows * sizeof(float) + 256;
+}
+
+template <class T, int D, int GB>
+static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
+                                   hipStream_t st) {
+  const int G = a.num_heads / a.num_kv_heads;
+  const int64_t nblk = (int64_t)ws.nsplit * (G / GB) * a.num_kv_heads * a.batch;
+  if (nblk > 0) {  // max_seq_len == 0: the combine alone writes zeros
+    hipLaunchKernelGGL((decode_split_kernel<T, D, GB>), dim3((unsigned)nblk), dim3(256), 0, st,
+                       a, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.batch * a.num_heads)),
+                     dim3(64), 0, st, a, ws);
+  return hipGetLastError();
+}
+
+template <class T, int D>
+static hipError_t launch_decode_d(const fa_decode_args& a, DecodeWs ws, hipStream_t st) {
+  switch (decode_group_size(a)) {
+    case 8: return launch_decode_gb<T, D, 8>(a, ws, st);
+    case 4: return launch_decode_gb<T, D, 4>(a, ws, st);
+    case 2: return launch_decode_gb<T, D, 2>(a, ws, st);
+    default: return launch_decode_gb<T, D, 1>(a, ws, st);
+  }
+}
+
+template <class T>
+static hipError_t launch_decode_t(const fa_decode_args& a, DecodeWs ws, hipStream_t st) {
+  switch (a.head_dim) {
+    case 64: return launch_decode_d<T, 64>(a, ws, st);
+    case 128: return launch_decode_d<T, 128>(a, ws, st);
+    case 256: return launch_decode_d<T, 256>(a, ws, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode(const fa_decode_args& a, void* workspace, hipStream_t st) {
+  DecodeWs ws;
+  ws.nsplit = decode_num_splits(a);
+  const size_t rows = (size_t)a.batch * a.num_heads * (size_t)ws.nsplit;
+  char* base = static_cast<char*>(workspace);
+  ws.po = reinterpret_cast<float*>(base);
+  ws.plse = reinterpret_cast<float*>(base + rows * a.head_dim * sizeof(float));
+  return a.dtype == FA_DTYPE_BF16 ? launch_decode_t<BFloat16>(a, ws, st)
+                                  : launch_decode_t<Half>(a, ws, st);
+}
+
+}  // namespace fa

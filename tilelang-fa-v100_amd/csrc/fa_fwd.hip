@@ -1,0 +1,271 @@
+// Dense and paged (vLLM) attention forward kernels for gfx950.
+//
+// Dense:  replaces _forward_lse_kernel_func (tilelang_fa_v100/
+//         _kernels_forward.py:94-172).  q/k/v/out are read and written in the
+//         caller's [B, S, H, D] layout through strides, so the four layout
+//         copies of interface.py:19-21,38 disappear.
+// Paged:  replaces _paged_kernel_func (_kernels_paged.py:193-344).  The
+//         grid is sized by total query rows, not rows x batch
+//         (_paged_adapter.py:44), and each workgroup finds its sequence with a
+//         scan over query_start_loc.  The Hq/Hkv query heads that share a KV
+//         head are packed into one row space (row = token * G + g), so every
+//         K/V tile fetched from the cache serves the whole GQA group.
+#include "fa_fwd_core.h"
+#include "fa_internal.h"
+
+namespace fa {
+
+struct DenseRows {
+  const uint16_t* q;
+  uint16_t* o;
+  float* lse;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t qs, os, ks, vs;  // per-row (sequence) strides, elements
+  int nrows, sk, off;      // off = seqlen_k - seqlen_q
+  bool causal, has_lse;
+
+  __device__ int kv_lo(int) const { return 0; }
+  __device__ int kv_hi(int r) const {
+    return causal ? min(max(r + off + 1, 0), sk) : sk;
+  }
+  __device__ const uint16_t* q_ptr(int r) const { return q + r * qs; }
+  __device__ uint16_t* o_ptr(int r) const { return o + r * os; }
+  __device__ float* lse_ptr(int r) const { return lse + r; }
+  __device__ const uint16_t* k_ptr(int n) const { return k + n * ks; }
+  __device__ const uint16_t* v_ptr(int n) const { return v + n * vs; }
+};
+
+template <class T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void fwd_dense_kernel(fa_fwd_args a) {
+  using S = FwdShape<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
+  const int qtiles = (a.seqlen_q + S::BM - 1) / S::BM;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt_raw = id % qtiles;
+  const int bh = id / qtiles;
+  const int h = bh % a.num_heads;
+  const int b = bh / a.num_heads;
+  // Heaviest causal tiles (largest query index) first.
+  const int qt = CAUSAL ? qtiles - 1 - qt_raw : qt_raw;
+  const int hk = h / (a.num_heads / a.num_heads_k);
+
+  DenseRows P;
+  P.q = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] + h * a.q_stride[2];
+  P.o = static_cast<uint16_t*>(a.out) + b * a.o_stride[0] + h * a.o_stride[2];
+  P.lse = a.lse ? a.lse + ((int64_t)b * a.num_heads + h) * a.seqlen_q : nullptr;
+  P.k = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
+  P.v = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
+  P.qs = a.q_stride[1];
+  P.os = a.o_stride[1];
+  P.ks = a.k_stride[1];
+  P.vs = a.v_stride[1];
+  P.nrows = a.seqlen_q;
+  P.sk = a.seqlen_k;
+  P.off = a.seqlen_k - a.seqlen_q;
+  P.causal = CAUSAL;
+  P.has_lse = a.lse != nullptr;
+  attn_fwd_tile<T, D>(P, qt * S::BM, a.softmax_scale, smem);
+}
+
+struct PagedRows {
+  const uint16_t* q;  // token 0 of the sequence, head hk*G
+  uint16_t* o;
+  float* lse;         // [Hq, num_tokens] at head hk*G, token 0 of the sequence
+  int64_t q_tok, q_head, o_tok, o_head, lse_head;
+  const uint16_t* kc;  // head hk
+  const uint16_t* vc;
+  int64_t k_page, k_slot, v_page, v_slot;
+  const int32_t* bt;   // block_table row of the sequence
+  int ps_log2, ps_mask, last_page;
+  int G, nrows, seq_len, prefix, wq, wk;
+  bool causal, has_lse;
+
+  __device__ int kv_lo(int r) const {
+    if (!causal || wq <= 0) return 0;
+    return max(0, r / G - wq + 1);
+  }
+  __device__ int kv_hi(int r) const {
+    const int t = r / G;
+    int hi = seq_len;
+    if (causal) hi = min(hi, prefix + t + 1);
+    if (causal && wk > 0) hi = min(hi, t + wk);
+    return hi;
+  }
+  __device__ const uint16_t* q_ptr(int r) const {
+    const int t = r / G;
+    return q + t * q_tok + (r - t * G) * q_head;
+  }
+  __device__ uint16_t* o_ptr(int r) const {
+    const int t = r / G;
+    return o + t * o_tok + (r - t * G) * o_head;
+  }
+  __device__ float* lse_ptr(int r) const {
+    const int t = r / G;
+    return lse + (r - t * G) * lse_head + t;
+  }
+  __device__ int64_t page_of(int n) const {
+    // Clamp guards against a corrupt table; valid tables are unaffected.
+    return (int64_t)min((unsigned)bt[n >> ps_log2], (unsigned)last_page);
+  }
+  __device__ const uint16_t* k_ptr(int n) const {
+    return kc + page_of(n) * k_page + (n & ps_mask) * k_slot;
+  }
+  __device__ const uint16_t* v_ptr(int n) const {
+    return vc + page_of(n) * v_page + (n & ps_mask) * v_slot;
+  }
+};
+
+// Finds the sequence owning `tile` in the varlen tile space where sequence b
+// has ceil(qlen_b * G / BM) tiles.  Returns b (or -1) and the tile index
+// within the sequence.  Block-wide scan over query_start_loc in LDS.
+__device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
+                             int tile, int* local) {
+  __shared__ int scan[256];
+  __shared__ int found_b, found_local, chunk_total;
+  const int tid = threadIdx.x;
+  if (tid == 0) found_b = -1;
+  int base = 0;
+  for (int c0 = 0; c0 < batch; c0 += 256) {
+    const int b = c0 + tid;
+    int n = 0;
+    if (b < batch) {
+      const int ql = qsl[b + 1] - qsl[b];
+      n = ql > 0 ? (int)(((int64_t)ql * G + BM - 1) / BM) : 0;
+    }
+    scan[tid] = n;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const int add = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += add;
+      __syncthreads();
+    }
+    const int incl = scan[tid];
+    const int excl = incl - n;
+    if (b < batch && n > 0 && tile >= base + excl && tile < base + incl) {
+      found_b = b;
+      found_local = tile - base - excl;
+    }
+    if (tid == 255) chunk_total = incl;
+    __syncthreads();
+    if (found_b >= 0) break;
+    base += chunk_total;
+    __syncthreads();
+  }
+  *local = found_local;
+  return found_b;
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(256) void fwd_paged_kernel(fa_paged_args a) {
+  using S = FwdShape<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
+  const int G = a.num_heads / a.num_kv_heads;
+  const int slots = gridDim.x / a.num_kv_heads;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int hk = id / slots;
+  const int slot = id % slots;
+
+  int local = 0;
+  const int b = find_sequence(a.query_start_loc, a.batch, G, S::BM, slot, &local);
+  if (b < 0) return;
+  const int qs = a.query_start_loc[b];
+  const int qlen = a.query_start_loc[b + 1] - qs;
+  const int ntiles = (int)(((int64_t)qlen * G + S::BM - 1) / S::BM);
+  // Later tiles of a causal sequence see more keys: run them first.
+  const int tile = ntiles - 1 - local;
+
+  PagedRows P;
+  P.G = G;
+  P.nrows = qlen * G;
+  P.q = static_cast<const uint16_t*>(a.q) + (int64_t)qs * a.q_stride[0] +
+        (int64_t)hk * G * a.q_stride[1];
+  P.o = static_cast<uint16_t*>(a.out) + (int64_t)qs * a.o_stride[0] +
+        (int64_t)hk * G * a.o_stride[1];
+  P.q_tok = a.q_stride[0];
+  P.q_head = a.q_stride[1];
+  P.o_tok = a.o_stride[0];
+  P.o_head = a.o_stride[1];
+  P.has_lse = a.lse != nullptr;
+  P.lse = a.lse ? a.lse + (int64_t)hk * G * a.num_tokens + qs : nullptr;
+  P.lse_head = a.num_tokens;
+  P.kc = static_cast<const uint16_t*>(a.k_cache) + (int64_t)hk * a.k_stride[2];
+  P.vc = static_cast<const uint16_t*>(a.v_cache) + (int64_t)hk * a.v_stride[2];
+  P.k_page = a.k_stride[0];
+  P.k_slot = a.k_stride[1];
+  P.v_page = a.v_stride[0];
+  P.v_slot = a.v_stride[1];
+  P.bt = a.block_table + (int64_t)b * a.block_table_stride;
+  P.ps_log2 = __builtin_ctz(a.page_size);
+  P.ps_mask = a.page_size - 1;
+  P.last_page = a.num_pages - 1;
+  // Keys beyond the block table's reach cannot be resolved; they are treated
+  // as absent.
+  P.seq_len = max(0, min(a.seq_lens[b], a.max_blocks * a.page_size));
+  P.prefix = a.prefix_kv_lens[b];
+  P.causal = a.causal != 0;
+  P.wq = a.window_q;
+  P.wk = a.window_k;
+  attn_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale, smem);
+}
+
+// ----------------------------------------------------------------- launchers
+
+template <class T, int D>
+static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
+  using S = FwdShape<D>;
+  const int qtiles = (a.seqlen_q + S::BM - 1) / S::BM;
+  const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
+  if (a.causal)
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, false>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <class T>
+static hipError_t dispatch_dense_d(const fa_fwd_args& a, hipStream_t st) {
+  switch (a.head_dim) {
+    case 64: return launch_dense<T, 64>(a, st);
+    case 128: return launch_dense<T, 128>(a, st);
+    case 256: return launch_dense<T, 256>(a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st) {
+  return a.dtype == FA_DTYPE_BF16 ? dispatch_dense_d<BFloat16>(a, st)
+                                  : dispatch_dense_d<Half>(a, st);
+}
+
+int paged_grid_slots(const fa_paged_args& a) {
+  const int G = a.num_heads / a.num_kv_heads;
+  const int64_t rows = (int64_t)a.num_tokens * G;
+  // sum_b ceil(rows_b / BM) <= ceil(rows / BM) + batch
+  return (int)((rows + 127) / 128 + a.batch);
+}
+
+template <class T, int D>
+static hipError_t launch_paged(const fa_paged_args& a, hipStream_t st) {
+  const dim3 grid((unsigned)paged_grid_slots(a) * a.num_kv_heads);
+  hipLaunchKernelGGL((fwd_paged_kernel<T, D>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <class T>
+static hipError_t dispatch_paged_d(const fa_paged_args& a, hipStream_t st) {
+  switch (a.head_dim) {
+    case 64: return launch_paged<T, 64>(a, st);
+    case 128: return launch_paged<T, 128>(a, st);
+    case 256: return launch_paged<T, 256>(a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_paged_prefill(const fa_paged_args& a, hipStream_t st) {
+  return a.dtype == FA_DTYPE_BF16 ? dispatch_paged_d<BFloat16>(a, st)
+                                  : dispatch_paged_d<Half>(a, st);
+}
+
+}  // namespace fa

@@ -1,0 +1,245 @@
+// Online-softmax attention forward for one 128-row query tile (gfx950).
+//
+// Algorithm (FlashAttention-2 forward, as in the reference
+// tilelang_fa_v100/_kernels_forward.py:94-172 and the paged variant
+// _kernels_paged.py:193-344): for each key tile, S = Q K^T (fp32 MFMA
+// accumulate), running row max m and row sum l, O <- O * exp(m_old - m_new)
+// + exp(S - m_new) V, and in the epilogue O / l and LSE = m * scale + ln l.
+//
+// Layout choices (see fa_common.h for the MFMA lane layout):
+//  * Four waves per workgroup; wave w owns query rows row0 + 32w .. +31 and
+//    lane (lr, lh) owns query row row0 + 32w + lr.
+//  * The kernel computes S^T = K Q^T (A = K from LDS, B = Q in registers), so
+//    every score a lane holds belongs to its own query row.  The row max
+//    therefore needs a single exchange with lane ^ 32 and the row sum none.
+//  * The probabilities P^T are kept in registers and used directly as the B
+//    operand of O^T = V^T P^T; V is stored transposed in LDS (keys
+//    contiguous) so the A operand is two 8-byte LDS reads.
+//  * K and V^T tiles are double-buffered in LDS; the next tile's global loads
+//    are issued before the current tile's MFMAs (one barrier per tile).
+//  * Visibility of key n to row r is an interval [kv_lo(r), kv_hi(r)) that is
+//    non-decreasing in r.  That covers dense causal (bottom-right), the paged
+//    prefix-anchored causal mask, sliding windows and plain length limits,
+//    and lets whole tiles be skipped or left unmasked from two row bounds.
+#pragma once
+
+#include "fa_common.h"
+
+namespace fa {
+
+template <int D>
+struct FwdShape {
+  static constexpr int BM = 128;           // query rows per workgroup
+  static constexpr int BN = 8192 / D;      // keys per tile (64 for D=128)
+  static constexpr int KS = D + 8;         // LDS row stride of K, elements
+  static constexpr int VS = BN + 4;        // LDS row stride of V^T, elements
+  static constexpr int KT = BN / 32;       // 32-key sub-tiles of S^T
+  static constexpr int DC = D / 16;        // 16-wide d chunks (QK^T)
+  static constexpr int DT = D / 32;        // 32-wide d tiles of O^T
+  static constexpr int KC = BN / 16;       // 16-key chunks (PV)
+  static constexpr int CPR = D / 8;        // 16-byte chunks per row
+  static constexpr int RSTEP = 256 / CPR;  // rows between a thread's K chunks
+  static constexpr int LDS_ELEMS = 2 * BN * KS + 2 * D * VS;
+  static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
+  static_assert(BN * CPR == 4 * 256, "four 16-byte chunks per thread per tile");
+};
+
+// Prob must provide:
+//   int nrows;
+//   int kv_lo(int r), kv_hi(int r)      visible keys of valid row r
+//   const uint16_t* q_ptr(int r); uint16_t* o_ptr(int r); float* lse_ptr(int r)
+//   bool has_lse;
+//   const uint16_t* k_ptr(int n); const uint16_t* v_ptr(int n)
+template <class T, int D, class Prob>
+__device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
+                                              float scale, uint16_t* smem) {
+  using S = FwdShape<D>;
+  const float scale_log2 = scale * kLog2e;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  uint16_t* Ks = smem;                    // [2][BN][KS]
+  uint16_t* Vt = smem + 2 * S::BN * S::KS;  // [2][D][VS]
+
+  const int nrows = P.nrows;
+  const int row_last = min(row0 + S::BM, nrows) - 1;
+  const int wg_lo = P.kv_lo(row0);
+  const int wg_hi = P.kv_hi(row_last);
+
+  const int wrow0 = row0 + wave * 32;
+  const bool wave_active = wrow0 < nrows;
+  const int wrow_last = min(wrow0 + 31, nrows - 1);
+  const int w_lo_min = wave_active ? P.kv_lo(wrow0) : 0;
+  const int w_lo_max = wave_active ? P.kv_lo(wrow_last) : 0;
+  const int w_hi_min = wave_active ? P.kv_hi(wrow0) : 0;
+  const int w_hi_max = wave_active ? P.kv_hi(wrow_last) : 0;
+
+  const int row = wrow0 + lr;
+  const bool row_valid = row < nrows;
+  const int my_lo = row_valid ? P.kv_lo(row) : 0;
+  const int my_hi = row_valid ? P.kv_hi(row) : 0;
+
+  // Q rows straight from HBM into the B-operand layout.
+  u32x4 qf[S::DC];
+  {
+    const uint16_t* qp = row_valid ? P.q_ptr(row) : nullptr;
+#pragma unroll
+    for (int c = 0; c < S::DC; ++c)
+      qf[c] = row_valid ? ld16(qp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
+  }
+
+  f32x16 o[S::DT];
+#pragma unroll
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  float m_run = neg_inf();
+  float l_run = 0.f;
+
+  // Cooperative tile loader: thread t owns the 16-byte column chunk
+  // col8 = t % CPR; K rows r0 + i*RSTEP and V rows 4*r0 + i (four consecutive
+  // keys, so V can be transposed in registers before the LDS store).
+  const int col8 = tid % S::CPR;
+  const int r0 = tid / S::CPR;
+  u32x4 kreg[4], vreg[4];
+  const int ld_hi = wg_hi;  // rows >= ld_hi are never dereferenced
+
+  auto load_tile = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + r0 + i * S::RSTEP;
+      kreg[i] = (n < ld_hi) ? ld16(P.k_ptr(n) + col8 * 8) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + 4 * r0 + i;
+      vreg[i] = (n < ld_hi) ? ld16(P.v_ptr(n) + col8 * 8) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* kb = Ks + buf * S::BN * S::KS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      st16(kb + (r0 + i * S::RSTEP) * S::KS + col8 * 8, kreg[i]);
+    uint16_t* vb = Vt + buf * D * S::VS;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int w = j >> 1;
+      u32x2 pr;
+      if (j & 1) {
+        pr[0] = pack_hi(vreg[0][w], vreg[1][w]);
+        pr[1] = pack_hi(vreg[2][w], vreg[3][w]);
+      } else {
+        pr[0] = pack_lo(vreg[0][w], vreg[1][w]);
+        pr[1] = pack_lo(vreg[2][w], vreg[3][w]);
+      }
+      st8(vb + (col8 * 8 + j) * S::VS + 4 * r0, pr);
+    }
+  };
+
+  const int j0 = max(wg_lo, 0) / S::BN;
+  const int j1 = (wg_hi + S::BN - 1) / S::BN;
+  if (j0 < j1) {
+    load_tile(j0 * S::BN);
+    store_tile(0);
+    __syncthreads();
+    for (int j = j0; j < j1; ++j) {
+      const int buf = (j - j0) & 1;
+      const bool more = j + 1 < j1;
+      if (more) load_tile((j + 1) * S::BN);
+      const int n0 = j * S::BN;
+      if (wave_active && n0 < w_hi_max && n0 + S::BN > w_lo_min) {
+        const uint16_t* kb = Ks + buf * S::BN * S::KS;
+        const uint16_t* vb = Vt + buf * D * S::VS;
+        f32x16 s[S::KT];
+#pragma unroll
+        for (int kt = 0; kt < S::KT; ++kt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
+#pragma unroll
+          for (int c = 0; c < S::DC; ++c) {
+            const u32x4 a = ld16(kb + (kt * 32 + lr) * S::KS + 16 * c + 8 * lh);
+            s[kt] = T::mma32(a, qf[c], s[kt]);
+          }
+        }
+        const bool need_mask = (n0 < w_lo_max) || (n0 + S::BN > w_hi_min);
+        if (need_mask) {
+#pragma unroll
+          for (int kt = 0; kt < S::KT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int kv = n0 + kt * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+              if (kv < my_lo || kv >= my_hi) s[kt][i] = neg_inf();
+            }
+        }
+        float mt = neg_inf();
+#pragma unroll
+        for (int kt = 0; kt < S::KT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kt][i]);
+        mt = fmaxf(mt, swap_halves(mt));
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = (m_new == neg_inf()) ? 0.f : m_new;
+        const float alpha = fast_exp2((m_run - m_use) * scale_log2);
+        const float mb = m_use * scale_log2;
+        float rs = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < S::KT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float p = fast_exp2(fmaf(s[kt][i], scale_log2, -mb));
+            s[kt][i] = p;
+            rs += p;
+          }
+        l_run = l_run * alpha + rs;
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+        m_run = m_new;
+
+        // P^T chunk kc holds keys 16kc + 8*(j/4) + 4*lh + (j%4), j = 0..7,
+        // which are accumulator entries 8*(kc%2) + j of sub-tile kc/2.
+        u32x4 pb[S::KC];
+#pragma unroll
+        for (int kc = 0; kc < S::KC; ++kc)
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            pb[kc][w] = T::pack(s[kc >> 1][8 * (kc & 1) + 2 * w],
+                                s[kc >> 1][8 * (kc & 1) + 2 * w + 1]);
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+          for (int kc = 0; kc < S::KC; ++kc) {
+            const uint16_t* vr = vb + (dt * 32 + lr) * S::VS + 16 * kc + 4 * lh;
+            const u32x2 lo8 = ld8(vr);
+            const u32x2 hi8 = ld8(vr + 8);
+            const u32x4 a = {lo8[0], lo8[1], hi8[0], hi8[1]};
+            o[dt] = T::mma32(a, pb[kc], o[dt]);
+          }
+      }
+      if (more) store_tile(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // Epilogue: both halves of the wave hold partial sums of the same row.
+  const float l_all = l_run + swap_halves(l_run);
+  if (!row_valid) return;
+  const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
+  uint16_t* op = P.o_ptr(row);
+#pragma unroll
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2 w;
+      w[0] = T::pack(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
+      w[1] = T::pack(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+      st8(op + 32 * dt + 8 * g + 4 * lh, w);
+    }
+  if (P.has_lse && lh == 0)
+    *P.lse_ptr(row) = l_all > 0.f ? m_run * scale + logf(l_all) : neg_inf();
+}
+
+}  // namespace fa

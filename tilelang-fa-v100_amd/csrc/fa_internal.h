@@ -1,0 +1,24 @@
+// Launchers behind the C ABI (fa_capi.cpp).  Arguments are validated by the
+// caller; these only configure grids and enqueue kernels on `st`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include "fa355.h"
+
+namespace fa {
+
+hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st);
+
+size_t bwd_workspace_bytes(const fa_bwd_args& a);
+hipError_t launch_bwd(const fa_bwd_args& a, void* ws, hipStream_t st);
+
+int paged_grid_slots(const fa_paged_args& a);
+hipError_t launch_paged_prefill(const fa_paged_args& a, hipStream_t st);
+
+int decode_num_splits(const fa_decode_args& a);
+size_t decode_workspace_bytes(const fa_decode_args& a);
+hipError_t launch_decode(const fa_decode_args& a, void* ws, hipStream_t st);
+
+}  // namespace fa

@@ -1,0 +1,22 @@
+"""MI355X (gfx950) FlashAttention, drop-in for the tilelang_fa_v100 API.
+
+The kernels are hand-written HIP in ../csrc, built into libfa355.so and called
+through a C ABI (include/fa355.h).  Exports match the reference package
+(tilelang_fa_v100/__init__.py:3-16).
+"""
+
+from .interface import (
+    FlashAttnTileLangVFunc,
+    tilelang_decode_forward,
+    tilelang_flash_attn_func,
+    tilelang_flash_attn_gpu,
+    tilelang_paged_forward,
+)
+
+__version__ = "1.0.0"
+__all__ = [
+    "tilelang_flash_attn_func",
+    "tilelang_flash_attn_gpu",
+    "tilelang_paged_forward",
+    "tilelang_decode_forward",
+]

@@ -1,0 +1,99 @@
+"""Host drivers of the dense forward / backward kernels.
+
+Replace the host side of tilelang_forward_lse (tilelang_fa_v100/
+_kernels_forward.py:188-193, called from interface.py:35-36) and of
+tilelang_backward (_kernels_backward.py:200-208).  Tensors stay in the FA2
+layout [B, S, H, D]; the kernels address them through strides, so the
+reference's permute/contiguous copies (interface.py:19-21,38,51) are gone.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._checks import HEAD_DIMS, rows_ready, strides
+
+
+def check_shapes(q, k, v):
+    """Validates [B, S, H, D] shapes; returns (B, Sq, Sk, H, Hk, D)."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D [batch, seqlen, heads, head_dim]")
+    B, Sq, H, D = q.shape
+    if k.shape != v.shape:
+        raise ValueError(f"k shape {tuple(k.shape)} differs from v shape {tuple(v.shape)}")
+    if k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"k shape {tuple(k.shape)} incompatible with q shape {tuple(q.shape)}")
+    Hk = k.shape[2]
+    if Hk == 0 or H % Hk != 0:
+        raise ValueError(f"num_heads {H} is not a multiple of num_heads_k {Hk}")
+    if D not in HEAD_DIMS:
+        raise ValueError(f"head_dim {D} not supported (expected one of {HEAD_DIMS})")
+    return B, Sq, k.shape[1], H, Hk, D
+
+
+def forward(q, k, v, softmax_scale: float, causal: bool):
+    """Returns (out [B,Sq,H,D], lse [B,H,Sq] fp32)."""
+    B, Sq, Sk, H, Hk, D = check_shapes(q, k, v)
+    q, k, v = rows_ready(q), rows_ready(k), rows_ready(v)
+    out = torch.empty((B, Sq, H, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+    a = _lib.FwdArgs()
+    a.q, a.k, a.v, a.out, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.q_stride[:] = strides(q, 3)
+    a.k_stride[:] = strides(k, 3)
+    a.v_stride[:] = strides(v, 3)
+    a.o_stride[:] = strides(out, 3)
+    a.batch, a.seqlen_q, a.seqlen_k = B, Sq, Sk
+    a.num_heads, a.num_heads_k, a.head_dim = H, Hk, D
+    a.softmax_scale = float(softmax_scale)
+    a.causal = int(bool(causal))
+    a.dtype = _lib.dtype_code(q.dtype)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.fa_fwd(ctypes.byref(a), _lib.stream_handle(q.device)), "fa_fwd")
+    return out, lse
+
+
+def bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic):
+    B, Sq, Sk, H, Hk, D = check_shapes(q, k, v)
+    a = _lib.BwdArgs()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.out, a.dout, a.lse = out.data_ptr(), dout.data_ptr(), lse.data_ptr()
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", out), ("do", dout),
+                    ("dq", dq), ("dk", dk), ("dv", dv)):
+        getattr(a, f"{name}_stride")[:] = strides(t, 3)
+    a.batch, a.seqlen_q, a.seqlen_k = B, Sq, Sk
+    a.num_heads, a.num_heads_k, a.head_dim = H, Hk, D
+    a.softmax_scale = float(softmax_scale)
+    a.causal = int(bool(causal))
+    a.dtype = _lib.dtype_code(q.dtype)
+    a.deterministic = int(bool(deterministic))
+    return a
+
+
+def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
+             deterministic: bool = False):
+    """Returns (dq, dk, dv), each contiguous [B, S, H, D] in q's dtype."""
+    if q.shape[-1] not in (64, 128):
+        raise NotImplementedError(f"backward for head_dim {q.shape[-1]} is not implemented "
+                                  "(supported: 64, 128)")
+    q, k, v, out, dout = (rows_ready(t) for t in (q, k, v, out, dout))
+    if dout.dtype != q.dtype:
+        dout = dout.to(q.dtype)
+    lse = lse.contiguous()
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    a = bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic)
+    lib = _lib.load()
+    nbytes = lib.fa_bwd_workspace_bytes(ctypes.byref(a))
+    if nbytes == 0:
+        _lib.check(_lib.FA_E_INVALID, "fa_bwd_workspace_bytes")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), nbytes,
+                              _lib.stream_handle(q.device)), "fa_bwd")
+    return dq, dk, dv
