@@ -53,6 +53,13 @@ struct Half {
     v[1] = (_Float16)hi;
     return __builtin_bit_cast(uint32_t, v);
   }
+  // Row-sum update for two probabilities p0, p1 whose packed form is w.
+  // fp16 keeps 11 significant bits, so summing the rounded values (one
+  // v_dot2_f32_f16 with ones) moves the LSE by at most 2^-11.
+  __device__ __forceinline__ static float sum2(float, float, uint32_t w, float acc) {
+    const f16x2 one = {(_Float16)1.f, (_Float16)1.f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+  }
   __device__ __forceinline__ static float lo(uint32_t w) {
     return (float)__builtin_bit_cast(f16x2, w)[0];
   }
@@ -76,6 +83,10 @@ struct BFloat16 {
     v[0] = (__bf16)lo;
     v[1] = (__bf16)hi;
     return __builtin_bit_cast(uint32_t, v);
+  }
+  // bf16 keeps 8 significant bits: the row sum uses the fp32 values.
+  __device__ __forceinline__ static float sum2(float p0, float p1, uint32_t, float acc) {
+    return acc + p0 + p1;
   }
   __device__ __forceinline__ static float lo(uint32_t w) {
     return __builtin_bit_cast(float, w << 16);

@@ -6,8 +6,10 @@
 // workgroup owns (fixed-size key chunk, KV head, head group, sequence):
 //   * all GB query heads of a GQA group are served by one read of the chunk's
 //     K and V rows (GB = largest of 8/4/2/1 dividing Hq/Hkv);
-//   * phase 1: S^T = K Q^T on the 16x16x32 MFMA (A = K rows straight from
-//     the paged cache, 16-byte loads; B = Q^T, unused head columns zero);
+//   * every K and V load of the chunk is issued first (16 + 16 vectors of
+//     16 bytes per lane), so a workgroup keeps its whole chunk in flight;
+//   * phase 1: S^T = K Q^T on the 16x16x32 MFMA (A = K rows from the paged
+//     cache in registers; B = Q^T, unused head columns zero);
 //   * phase 2: per-head max / exp2 / sum over the chunk in LDS;
 //   * phase 3: O += P V on the VALU, each lane owning 8 contiguous d of a V
 //     row, followed by a cross-lane and cross-wave reduction;
@@ -20,7 +22,21 @@
 
 namespace fa {
 
-constexpr int kDecChunk = 256;  // keys per split workgroup
+// Keys per split workgroup: every lane then holds 16 K and 16 V vectors of
+// 16 bytes (32768 / D keys for any D), all loads issued before any use.
+template <int D>
+struct DecShape {
+  static constexpr int CH = 32768 / D;   // keys per chunk (256 for D=128)
+  static constexpr int DC = D / 32;      // 32-wide d chunks of the QK^T MFMA
+  static constexpr int KIT = CH / 64;    // 16-key blocks per wave (phase 1)
+  static constexpr int LPT = D / 8;      // lanes per V row (phase 3)
+  static constexpr int TPW = 64 / LPT;   // V rows per wave per pass
+  static constexpr int TPB = 4 * TPW;    // V rows per workgroup per pass
+  static constexpr int VIT = CH / TPB;   // passes (phase 3)
+  static_assert(KIT * DC == 16 && VIT == 16, "16 K and 16 V loads per lane");
+};
+
+__host__ __device__ constexpr int dec_chunk(int D) { return 32768 / D; }
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -40,14 +56,11 @@ struct DecodeWs {
 };
 
 template <class T, int D, int GB>
-__global__ __launch_bounds__(256) void decode_split_kernel(fa_decode_args a,
-                                                           DecodeWs ws) {
-  constexpr int CH = kDecChunk;
-  constexpr int LPT = D / 8;       // lanes per V row in phase 3
-  constexpr int TPW = 64 / LPT;    // rows per wave per pass in phase 3
-  constexpr int TPB = 4 * TPW;     // rows per workgroup per pass
-  constexpr int DC = D / 32;       // 32-wide d chunks of the QK^T MFMA
-  __shared__ float s_lds[GB][CH];
+__global__ __launch_bounds__(256, 2) void decode_split_kernel(fa_decode_args a,
+                                                              DecodeWs ws) {
+  using S = DecShape<D>;
+  constexpr int CH = S::CH;
+  __shared__ __attribute__((aligned(16))) float s_lds[GB][CH];
   __shared__ float red[4][GB][D];
   __shared__ float stat_m[GB], stat_l[GB];
 
@@ -65,6 +78,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(fa_decode_args a,
   const int n_begin = c * CH;
   if (n_begin >= seq_len) return;
   const int n_end = min(n_begin + CH, seq_len);
+  const int n_last = n_end - 1;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h0 = hk * G + hg * GB;  // first query head of this group
@@ -74,37 +88,51 @@ __global__ __launch_bounds__(256) void decode_split_kernel(fa_decode_args a,
   const int ps_log2 = __builtin_ctz(a.page_size);
   const int ps_mask = a.page_size - 1;
   const unsigned last_page = (unsigned)(a.num_pages - 1);
-  auto page_of = [&](int n) -> int64_t {
-    return (int64_t)min((unsigned)bt[n >> ps_log2], last_page);
+  // Keys past the chunk end are read from its last key (finite data that is
+  // masked or multiplied by P = 0), so every load is unconditional.
+  auto row_of = [&](const uint16_t* base, int64_t page_stride, int64_t slot_stride,
+                    int n) -> const uint16_t* {
+    n = min(n, n_last);
+    const int64_t page = (int64_t)min((unsigned)bt[n >> ps_log2], last_page);
+    return base + page * page_stride + (n & ps_mask) * slot_stride;
   };
   const float scale_log2 = a.softmax_scale * kLog2e;
 
-  // ---- phase 1: scores.  Wave w handles 16-key blocks w, w+4, ...
+  // ---- issue every load of the chunk: K in MFMA-A layout, V rows for phase 3.
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int lsub = lane % S::LPT, lrow = lane / S::LPT;
+  u32x4 kr[S::KIT][S::DC], vr[S::VIT];
+#pragma unroll
+  for (int it = 0; it < S::KIT; ++it) {
+    const uint16_t* kp = row_of(kc, a.k_stride[0], a.k_stride[1],
+                                n_begin + (wave + 4 * it) * 16 + l16);
+#pragma unroll
+    for (int cc = 0; cc < S::DC; ++cc) kr[it][cc] = ld16(kp + 32 * cc + 8 * lq);
+  }
+#pragma unroll
+  for (int it = 0; it < S::VIT; ++it) {
+    const uint16_t* vp = row_of(vc, a.v_stride[0], a.v_stride[1],
+                                n_begin + it * S::TPB + wave * S::TPW + lrow);
+    vr[it] = ld16(vp + 8 * lsub);
+  }
+
+  // ---- phase 1: S^T = K Q^T on the 16x16x32 MFMA (columns = query heads).
   {
-    const int l16 = lane & 15, lq = lane >> 4;
-    u32x4 qb[DC];
+    u32x4 qb[S::DC];
     const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_stride[0] +
-                           (int64_t)(h0 + l16) * a.q_stride[1];
+                           (int64_t)(h0 + min(l16, GB - 1)) * a.q_stride[1];
 #pragma unroll
-    for (int cc = 0; cc < DC; ++cc)
-      qb[cc] = (l16 < GB) ? ld16(qrow + 32 * cc + 8 * lq) : u32x4{0, 0, 0, 0};
+    for (int cc = 0; cc < S::DC; ++cc) {
+      const u32x4 qv = ld16(qrow + 32 * cc + 8 * lq);
+      qb[cc] = (l16 < GB) ? qv : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
-    for (int it = 0; it < CH / 64; ++it) {
+    for (int it = 0; it < S::KIT; ++it) {
       const int blk = wave + 4 * it;
-      const int n = n_begin + blk * 16 + l16;
-      u32x4 kr[DC];
-      if (n < n_end) {
-        const uint16_t* kp = kc + page_of(n) * a.k_stride[0] + (n & ps_mask) * a.k_stride[1];
-#pragma unroll
-        for (int cc = 0; cc < DC; ++cc) kr[cc] = ld16(kp + 32 * cc + 8 * lq);
-      } else {
-#pragma unroll
-        for (int cc = 0; cc < DC; ++cc) kr[cc] = u32x4{0, 0, 0, 0};
-      }
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int cc = 0; cc < DC; ++cc) acc = T::mma16(kr[cc], qb[cc], acc);
-      // acc[i] = S^T[key = 4*lq + i][head = l16]
+      for (int cc = 0; cc < S::DC; ++cc) acc = T::mma16(kr[it][cc], qb[cc], acc);
+      // acc[i] = S^T[key = blk*16 + 4*lq + i][head = l16]
       if (l16 < GB) {
         f32x4 sv;
 #pragma unroll
@@ -137,38 +165,31 @@ __global__ __launch_bounds__(256) void decode_split_kernel(fa_decode_args a,
   }
   __syncthreads();
 
-  // ---- phase 3: O = P V.  LPT lanes per key row, 8 d per lane.
-  const int lsub = lane % LPT;
-  const int lrow = lane / LPT;
+  // ---- phase 3: O = P V on the VALU, 8 d per lane.
   float acc[GB][8];
 #pragma unroll
   for (int g = 0; g < GB; ++g)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
 #pragma unroll
-  for (int t0 = 0; t0 < CH; t0 += TPB) {
-    const int t = t0 + wave * TPW + lrow;
-    const int n = n_begin + t;
-    if (n < n_end) {
-      const uint16_t* vp = vc + page_of(n) * a.v_stride[0] + (n & ps_mask) * a.v_stride[1];
-      const u32x4 vr = ld16(vp + 8 * lsub);
-      float vf[8];
+  for (int it = 0; it < S::VIT; ++it) {
+    const int t = it * S::TPB + wave * S::TPW + lrow;
+    float vf[8];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        vf[2 * w] = T::lo(vr[w]);
-        vf[2 * w + 1] = T::hi(vr[w]);
-      }
+    for (int w = 0; w < 4; ++w) {
+      vf[2 * w] = T::lo(vr[it][w]);
+      vf[2 * w + 1] = T::hi(vr[it][w]);
+    }
 #pragma unroll
-      for (int g = 0; g < GB; ++g) {
-        const float p = s_lds[g][t];
+    for (int g = 0; g < GB; ++g) {
+      const float p = s_lds[g][t];  // 0 for keys past the chunk end
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(p, vf[j], acc[g][j]);
-      }
+      for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(p, vf[j], acc[g][j]);
     }
   }
   // Reduce over the key rows held by lanes of equal lsub within the wave.
 #pragma unroll
-  for (int o = LPT; o < 64; o <<= 1)
+  for (int o = S::LPT; o < 64; o <<= 1)
 #pragma unroll
     for (int g = 0; g < GB; ++g)
 #pragma unroll
@@ -190,38 +211,49 @@ __global__ __launch_bounds__(256) void decode_split_kernel(fa_decode_args a,
   }
 }
 
-// One wave per (sequence, query head): merge the chunk partials.
+// One wave per (sequence, query head): merge the chunk partials with weights
+// exp2(lse_c - max), computed lane-parallel, then an unrolled weighted sum.
 template <class T, int D>
 __global__ __launch_bounds__(64) void decode_combine_kernel(fa_decode_args a,
                                                             DecodeWs ws) {
+  constexpr int CH = dec_chunk(D);
+  constexpr int NP = (D + 127) / 128;  // d pairs per lane: 2*lane + 128*k
+  __shared__ float wts[64];
   const int hq = blockIdx.x % a.num_heads;
   const int b = blockIdx.x / a.num_heads;
   const int lane = threadIdx.x;
   const int seq_len = max(0, min(a.seq_lens[b], a.max_blocks * a.page_size));
-  const int ns = (seq_len + kDecChunk - 1) / kDecChunk;
+  const int ns = (seq_len + CH - 1) / CH;
   const int64_t row0 = ((int64_t)b * a.num_heads + hq) * ws.nsplit;
   float m = neg_inf();
   for (int c = lane; c < ns; c += 64) m = fmaxf(m, ws.plse[row0 + c]);
   m = wave_max(m);
-  // Lane owns d pairs 2*lane + 128*k.
-  constexpr int NP = (D + 127) / 128;
+  const float m_use = (m == neg_inf()) ? 0.f : m;
   float acc[NP][2];
 #pragma unroll
   for (int k = 0; k < NP; ++k) acc[k][0] = acc[k][1] = 0.f;
   float wsum = 0.f;
-  const float m_use = (m == neg_inf()) ? 0.f : m;
-  for (int c = 0; c < ns; ++c) {
-    const float w = fast_exp2(ws.plse[row0 + c] - m_use);
-    wsum += w;
-    const float* pp = ws.po + (row0 + c) * D;
+  for (int c0 = 0; c0 < ns; c0 += 64) {
+    const int cn = min(64, ns - c0);
+    const float w = lane < cn ? fast_exp2(ws.plse[row0 + c0 + lane] - m_use) : 0.f;
+    wsum += wave_sum(w);
+    wts[lane] = w;
+    __syncthreads();
+    const float* base = ws.po + (row0 + c0) * D;
+#pragma unroll 8
+    for (int c = 0; c < cn; ++c) {
+      const float wc = wts[c];
 #pragma unroll
-    for (int k = 0; k < NP; ++k) {
-      const int d = 2 * lane + 128 * k;
-      if (d < D) {
-        acc[k][0] = fmaf(w, pp[d], acc[k][0]);
-        acc[k][1] = fmaf(w, pp[d + 1], acc[k][1]);
+      for (int k = 0; k < NP; ++k) {
+        const int d = 2 * lane + 128 * k;
+        if (d < D) {
+          const float2 pv = *reinterpret_cast<const float2*>(base + (int64_t)c * D + d);
+          acc[k][0] = fmaf(wc, pv.x, acc[k][0]);
+          acc[k][1] = fmaf(wc, pv.y, acc[k][1]);
+        }
       }
     }
+    __syncthreads();
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   uint16_t* op = static_cast<uint16_t*>(a.out) + (int64_t)b * a.o_stride[0] +
@@ -240,7 +272,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(fa_decode_args a,
 // ----------------------------------------------------------------- launchers
 
 int decode_num_splits(const fa_decode_args& a) {
-  return (a.max_seq_len + kDecChunk - 1) / kDecChunk;
+  const int ch = dec_chunk(a.head_dim);
+  return (a.max_seq_len + ch - 1) / ch;
 }
 
 int decode_group_size(const fa_decode_args& a) {

@@ -11,6 +11,7 @@
 //         head are packed into one row space (row = token * G + g), so every
 //         K/V tile fetched from the cache serves the whole GQA group.
 #include "fa_fwd_core.h"
+#include "fa_fwd_d128.h"
 #include "fa_internal.h"
 
 namespace fa {
@@ -36,11 +37,41 @@ struct DenseRows {
   __device__ const uint16_t* v_ptr(int n) const { return v + n * vs; }
 };
 
+// Tile geometry per head_dim: D = 128 uses the direct-to-LDS 8-wave core.
+template <int D>
+struct FwdKernelCfg {
+  static constexpr int BM = FwdShape<D>::BM;
+  static constexpr int THREADS = 256;
+  static constexpr int WAVES_PER_EU = FwdShape<D>::kWavesPerEU;
+  static constexpr int LDS_BYTES = FwdShape<D>::LDS_ELEMS * 2;
+};
+template <>
+struct FwdKernelCfg<128> {
+  static constexpr int BM = FwdShapeD128::BM;
+  static constexpr int THREADS = 512;
+  static constexpr int WAVES_PER_EU = 2;
+  static constexpr int LDS_BYTES = FwdShapeD128::LDS_BYTES;
+};
+
+// LDS: one array for the 4-wave core; four distinct arrays for the D = 128
+// core (see attn_fwd_tile_d128).
+template <class T, int D, class Prob>
+__device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scale) {
+  if constexpr (D == 128) {
+    constexpr int B = FwdShapeD128::LDS_ARRAY_BYTES;
+    __shared__ __attribute__((aligned(16))) char k0[B], v0[B], k1[B], v1[B];
+    attn_fwd_tile_d128<T>(P, row0, scale, k0, v0, k1, v1);
+  } else {
+    __shared__ __attribute__((aligned(16))) uint16_t smem[FwdShape<D>::LDS_ELEMS];
+    attn_fwd_tile<T, D>(P, row0, scale, smem);
+  }
+}
+
 template <class T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void fwd_dense_kernel(fa_fwd_args a) {
-  using S = FwdShape<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
-  const int qtiles = (a.seqlen_q + S::BM - 1) / S::BM;
+__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+void fwd_dense_kernel(fa_fwd_args a) {
+  using C = FwdKernelCfg<D>;
+  const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int qt_raw = id % qtiles;
   const int bh = id / qtiles;
@@ -65,7 +96,7 @@ __global__ __launch_bounds__(256) void fwd_dense_kernel(fa_fwd_args a) {
   P.off = a.seqlen_k - a.seqlen_q;
   P.causal = CAUSAL;
   P.has_lse = a.lse != nullptr;
-  attn_fwd_tile<T, D>(P, qt * S::BM, a.softmax_scale, smem);
+  run_fwd_tile<T, D>(P, qt * C::BM, a.softmax_scale);
 }
 
 struct PagedRows {
@@ -118,36 +149,43 @@ struct PagedRows {
 
 // Finds the sequence owning `tile` in the varlen tile space where sequence b
 // has ceil(qlen_b * G / BM) tiles.  Returns b (or -1) and the tile index
-// within the sequence.  Block-wide scan over query_start_loc in LDS.
+// within the sequence.  Threads 0..255 scan query_start_loc in LDS, 256
+// sequences per pass; the rest of the workgroup only joins the barriers.
 __device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
                              int tile, int* local) {
-  __shared__ int scan[256];
+  constexpr int NS = 256;
+  __shared__ int scan[NS];
   __shared__ int found_b, found_local, chunk_total;
   const int tid = threadIdx.x;
-  if (tid == 0) found_b = -1;
+  const bool act = tid < NS;
+  if (tid == 0) {
+    found_b = -1;
+    found_local = 0;
+  }
+  __syncthreads();
   int base = 0;
-  for (int c0 = 0; c0 < batch; c0 += 256) {
+  for (int c0 = 0; c0 < batch; c0 += NS) {
     const int b = c0 + tid;
     int n = 0;
-    if (b < batch) {
+    if (act && b < batch) {
       const int ql = qsl[b + 1] - qsl[b];
       n = ql > 0 ? (int)(((int64_t)ql * G + BM - 1) / BM) : 0;
     }
-    scan[tid] = n;
+    if (act) scan[tid] = n;
     __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int add = tid >= off ? scan[tid - off] : 0;
+    for (int off = 1; off < NS; off <<= 1) {
+      const int add = (act && tid >= off) ? scan[tid - off] : 0;
       __syncthreads();
-      scan[tid] += add;
+      if (act) scan[tid] += add;
       __syncthreads();
     }
-    const int incl = scan[tid];
+    const int incl = act ? scan[tid] : 0;
     const int excl = incl - n;
-    if (b < batch && n > 0 && tile >= base + excl && tile < base + incl) {
+    if (act && b < batch && n > 0 && tile >= base + excl && tile < base + incl) {
       found_b = b;
       found_local = tile - base - excl;
     }
-    if (tid == 255) chunk_total = incl;
+    if (tid == NS - 1) chunk_total = incl;
     __syncthreads();
     if (found_b >= 0) break;
     base += chunk_total;
@@ -158,9 +196,9 @@ __device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
 }
 
 template <class T, int D>
-__global__ __launch_bounds__(256) void fwd_paged_kernel(fa_paged_args a) {
-  using S = FwdShape<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
+__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+void fwd_paged_kernel(fa_paged_args a) {
+  using S = FwdKernelCfg<D>;
   const int G = a.num_heads / a.num_kv_heads;
   const int slots = gridDim.x / a.num_kv_heads;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -207,20 +245,20 @@ __global__ __launch_bounds__(256) void fwd_paged_kernel(fa_paged_args a) {
   P.causal = a.causal != 0;
   P.wq = a.window_q;
   P.wk = a.window_k;
-  attn_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale, smem);
+  run_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale);
 }
 
 // ----------------------------------------------------------------- launchers
 
 template <class T, int D>
 static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
-  using S = FwdShape<D>;
-  const int qtiles = (a.seqlen_q + S::BM - 1) / S::BM;
+  using C = FwdKernelCfg<D>;
+  const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
   if (a.causal)
-    hipLaunchKernelGGL((fwd_dense_kernel<T, D, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, true>), grid, dim3(C::THREADS), 0, st, a);
   else
-    hipLaunchKernelGGL((fwd_dense_kernel<T, D, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, false>), grid, dim3(C::THREADS), 0, st, a);
   return hipGetLastError();
 }
 
@@ -239,17 +277,26 @@ hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st) {
                                   : dispatch_dense_d<Half>(a, st);
 }
 
+int paged_block_rows(int head_dim) {
+  switch (head_dim) {
+    case 64: return FwdKernelCfg<64>::BM;
+    case 128: return FwdKernelCfg<128>::BM;
+    default: return FwdKernelCfg<256>::BM;
+  }
+}
+
 int paged_grid_slots(const fa_paged_args& a) {
   const int G = a.num_heads / a.num_kv_heads;
   const int64_t rows = (int64_t)a.num_tokens * G;
+  const int bm = paged_block_rows(a.head_dim);
   // sum_b ceil(rows_b / BM) <= ceil(rows / BM) + batch
-  return (int)((rows + 127) / 128 + a.batch);
+  return (int)((rows + bm - 1) / bm + a.batch);
 }
 
 template <class T, int D>
 static hipError_t launch_paged(const fa_paged_args& a, hipStream_t st) {
   const dim3 grid((unsigned)paged_grid_slots(a) * a.num_kv_heads);
-  hipLaunchKernelGGL((fwd_paged_kernel<T, D>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((fwd_paged_kernel<T, D>), grid, dim3(FwdKernelCfg<D>::THREADS), 0, st, a);
   return hipGetLastError();
 }
 

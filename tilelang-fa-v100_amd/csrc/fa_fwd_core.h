@@ -40,6 +40,8 @@ struct FwdShape {
   static constexpr int CPR = D / 8;        // 16-byte chunks per row
   static constexpr int RSTEP = 256 / CPR;  // rows between a thread's K chunks
   static constexpr int LDS_ELEMS = 2 * BN * KS + 2 * D * VS;
+  // Two workgroups per CU (2 waves per SIMD) fit the register file up to D=128.
+  static constexpr int kWavesPerEU = D <= 128 ? 2 : 1;
   static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
   static_assert(BN * CPR == 4 * 256, "four 16-byte chunks per thread per tile");
 };
@@ -55,6 +57,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
                                               float scale, uint16_t* smem) {
   using S = FwdShape<D>;
   const float scale_log2 = scale * kLog2e;
+  constexpr float kLazy = 8.f;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, lh = lane >> 5;
@@ -94,7 +97,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
   for (int dt = 0; dt < S::DT; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-  float m_run = neg_inf();
+  float ms_run = neg_inf();  // running row max * scale * log2(e)
   float l_run = 0.f;
 
   // Cooperative tile loader: thread t owns the 16-byte column chunk
@@ -103,18 +106,21 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
   const int col8 = tid % S::CPR;
   const int r0 = tid / S::CPR;
   u32x4 kreg[4], vreg[4];
-  const int ld_hi = wg_hi;  // rows >= ld_hi are never dereferenced
+  // Rows at or beyond wg_hi are never visible: they are loaded from the last
+  // visible row instead (finite data, multiplied by P = 0), which keeps every
+  // load unconditional and never touches memory past the keys.
+  const int ld_last = max(wg_hi - 1, 0);
 
   auto load_tile = [&](int n0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int n = n0 + r0 + i * S::RSTEP;
-      kreg[i] = (n < ld_hi) ? ld16(P.k_ptr(n) + col8 * 8) : u32x4{0, 0, 0, 0};
+      const int n = min(n0 + r0 + i * S::RSTEP, ld_last);
+      kreg[i] = ld16(P.k_ptr(n) + col8 * 8);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int n = n0 + 4 * r0 + i;
-      vreg[i] = (n < ld_hi) ? ld16(P.v_ptr(n) + col8 * 8) : u32x4{0, 0, 0, 0};
+      const int n = min(n0 + 4 * r0 + i, ld_last);
+      vreg[i] = ld16(P.v_ptr(n) + col8 * 8);
     }
   };
   auto store_tile = [&](int buf) {
@@ -173,41 +179,42 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
               if (kv < my_lo || kv >= my_hi) s[kt][i] = neg_inf();
             }
         }
+        // Running max in scaled base-2 units (ms).  A row's max only moves
+        // when the tile max exceeds it by more than kLazy, so P <= 2^kLazy
+        // (exact in fp16/bf16) and O is rescaled on few tiles.
         float mt = neg_inf();
 #pragma unroll
         for (int kt = 0; kt < S::KT; ++kt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kt][i]);
-        mt = fmaxf(mt, swap_halves(mt));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = (m_new == neg_inf()) ? 0.f : m_new;
-        const float alpha = fast_exp2((m_run - m_use) * scale_log2);
-        const float mb = m_use * scale_log2;
-        float rs = 0.f;
+        mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+        const bool grow = mt > ms_run + kLazy;
+        if (__any(grow)) {
+          const float ms_new = grow ? mt : ms_run;
+          const float alpha = grow ? fast_exp2(ms_run - ms_new) : 1.f;
+          ms_run = ms_new;
+          l_run *= alpha;
 #pragma unroll
-        for (int kt = 0; kt < S::KT; ++kt)
+          for (int dt = 0; dt < S::DT; ++dt)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float p = fast_exp2(fmaf(s[kt][i], scale_log2, -mb));
-            s[kt][i] = p;
-            rs += p;
-          }
-        l_run = l_run * alpha + rs;
-#pragma unroll
-        for (int dt = 0; dt < S::DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-        m_run = m_new;
-
+            for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+        }
+        // A row with no visible key so far has ms_run = -inf and only -inf
+        // scores in this tile: any finite offset gives P = 0.
+        const float mb = ms_run == neg_inf() ? 0.f : ms_run;
         // P^T chunk kc holds keys 16kc + 8*(j/4) + 4*lh + (j%4), j = 0..7,
         // which are accumulator entries 8*(kc%2) + j of sub-tile kc/2.
         u32x4 pb[S::KC];
 #pragma unroll
         for (int kc = 0; kc < S::KC; ++kc)
 #pragma unroll
-          for (int w = 0; w < 4; ++w)
-            pb[kc][w] = T::pack(s[kc >> 1][8 * (kc & 1) + 2 * w],
-                                s[kc >> 1][8 * (kc & 1) + 2 * w + 1]);
+          for (int w = 0; w < 4; ++w) {
+            const int e = 8 * (kc & 1) + 2 * w;
+            const float p0 = fast_exp2(fmaf(s[kc >> 1][e], scale_log2, -mb));
+            const float p1 = fast_exp2(fmaf(s[kc >> 1][e + 1], scale_log2, -mb));
+            pb[kc][w] = T::pack(p0, p1);
+            l_run = T::sum2(p0, p1, pb[kc][w], l_run);
+          }
 #pragma unroll
         for (int dt = 0; dt < S::DT; ++dt)
 #pragma unroll
@@ -239,7 +246,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
       st8(op + 32 * dt + 8 * g + 4 * lh, w);
     }
   if (P.has_lse && lh == 0)
-    *P.lse_ptr(row) = l_all > 0.f ? m_run * scale + logf(l_all) : neg_inf();
+    *P.lse_ptr(row) = l_all > 0.f ? (ms_run + log2f(l_all)) * kLn2 : neg_inf();
 }
 
 }  // namespace fa
