@@ -9,6 +9,8 @@
 // (_kernels_backward.py:72-74,159-170).  dQ is reduced across KV tiles with
 // fp32 atomics into a caller-provided workspace and converted afterwards.
 //
+// dQ is accumulated in fp32 in a [B, H, Sq, D] workspace.
+//
 // Kernels:
 //   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row; zeroes
 //                       the dQ accumulator rows it covers.
@@ -16,7 +18,9 @@
 //                       loops over the 64-row query tiles of every query
 //                       head that shares the KV head (GQA).  K and V of the wave stay in registers,
 //                       K^T of the workgroup stays in LDS.
+//   bwd_main_d128_kernel  head_dim 128 variant (fa_bwd_d128.h).
 //   bwd_dq_convert      dQ = scale * acc, cast to the input dtype.
+#include "fa_bwd_d128.h"
 #include "fa_common.h"
 #include "fa_internal.h"
 
@@ -321,8 +325,8 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     {
       const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
       if (any) {
-        float* dqb = dqacc + (((int64_t)b * Sq) * H + h) * D;
-        const int64_t qstride = (int64_t)H * D;
+        float* dqb = dqacc + ((int64_t)b * H + h) * Sq * D;  // [B, H, Sq, D]
+        const int64_t qstride = D;
 #pragma unroll
         for (int pr = wave; pr < S::NQT * S::DT; pr += 4) {
           const int qt = pr % S::NQT, dt = pr / S::NQT;
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(fa_bwd_args a,
   const int64_t bq = r / a.num_heads;
   const int q = (int)(bq % a.seqlen_q);
   const int b = (int)(bq / a.seqlen_q);
-  const float* src = dqacc + r * D + 8 * sub;
+  const float* src = dqacc + (((int64_t)b * a.num_heads + h) * a.seqlen_q + q) * D + 8 * sub;
   const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
   const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
   const float sc = a.softmax_scale;
@@ -415,16 +419,30 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, rowdot, lse2);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
-  const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
-  if (kvtiles == 0) {
-    // No keys: dQ stays zero; dK / dV are empty.
-  } else if (a.causal)
-    hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc,
-                       rowdot, lse2);
-  else
-    hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc,
-                       rowdot, lse2);
+  if constexpr (D == 128) {
+    using S2 = BwdShapeD128;
+    const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
+    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
+    if (kvtiles == 0) {
+      // No keys: dQ stays zero; dK / dV are empty.
+    } else if (a.causal)
+      hipLaunchKernelGGL((bwd_main_d128_kernel<T, true>), grid, dim3(512), 0, st, a, dqacc,
+                         rowdot, lse2);
+    else
+      hipLaunchKernelGGL((bwd_main_d128_kernel<T, false>), grid, dim3(512), 0, st, a, dqacc,
+                         rowdot, lse2);
+  } else {
+    const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
+    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
+    if (kvtiles == 0) {
+      // No keys: dQ stays zero; dK / dV are empty.
+    } else if (a.causal)
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc,
+                         rowdot, lse2);
+    else
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc,
+                         rowdot, lse2);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((bwd_dq_convert_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc);

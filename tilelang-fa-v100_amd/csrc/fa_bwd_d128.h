@@ -1,0 +1,293 @@
+// Attention backward main kernel for head_dim 128 on gfx950.
+//
+// Same mathematics as bwd_main_kernel (fa_bwd.hip): per (key tile, query
+// tile) the 5 products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS and
+// dQ += dS K, with P = exp2(S·scale·log2e − lse2) and dS = P (dP − rowdot).
+// Layout, for the gfx950 memory instructions:
+//  * 8 waves x 32 keys = 256 keys per workgroup, so the fp32 atomics that
+//    reduce dQ across key tiles cover 256 keys each.
+//  * The workgroup's K tile (256 x 256 B) is copied once HBM -> LDS with
+//    global_load_lds_dwordx4 and serves as the B operand of S (row reads)
+//    and of dQ (transpose reads).  V rows of each wave stay in registers.
+//  * Q and dO tiles (32 rows) are DMA'd the same way, double-buffered in
+//    distinct arrays (see attn_fwd_tile_d128 for why distinct arrays).
+//    Qᵀ / dOᵀ operands come from ds_read_b64_tr_b16; nothing is transposed
+//    in registers.
+//  * dSᵀ goes to LDS with 8-byte stores (its 8-byte pieces XOR-swizzled by
+//    row so both the stores and the transpose reads are conflict free) and
+//    is read back transposed as the A operand of dQ.
+//  * 256-byte K / Q / dO rows use the 16-byte-chunk swizzle of
+//    fa_fwd_d128.h.
+#pragma once
+
+#include "fa355.h"
+#include "fa_common.h"
+#include "fa_fwd_d128.h"
+
+namespace fa {
+
+struct BwdShapeD128 {
+  static constexpr int D = 128;
+  static constexpr int BKV = 256;  // keys per workgroup (32 per wave)
+  static constexpr int BQ = 32;    // query rows per iteration
+  static constexpr int ROWB = 256;
+  static constexpr int K_BYTES = BKV * ROWB;  // 64 KB
+  static constexpr int QT_BYTES = BQ * ROWB;  // 8 KB
+  static constexpr int DS_ROWB = BQ * 2;      // 64 B per dSᵀ row
+  static constexpr int DS_BYTES = BKV * DS_ROWB;
+};
+
+// Byte offset of the 8-byte piece p (0..7) of dSᵀ row r.
+__device__ __forceinline__ int ds_piece(int r, int p) {
+  return r * BwdShapeD128::DS_ROWB + 8 * (p ^ ((r >> 2) & 7));
+}
+
+template <class T, bool CAUSAL>
+__global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc,
+                                                               const float* rowdot,
+                                                               const float* lse2) {
+  using S = BwdShapeD128;
+  constexpr int D = S::D;
+  __shared__ __attribute__((aligned(16))) char Ks[S::K_BYTES];
+  __shared__ __attribute__((aligned(16))) char Q0[S::QT_BYTES], O0[S::QT_BYTES];
+  __shared__ __attribute__((aligned(16))) char Q1[S::QT_BYTES], O1[S::QT_BYTES];
+  __shared__ __attribute__((aligned(16))) float st0[2 * S::BQ], st1[2 * S::BQ];
+  __shared__ __attribute__((aligned(16))) char dSt[S::DS_BYTES];
+
+  const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads, Hk = a.num_heads_k;
+  const int G = H / Hk;
+  const int kvtiles = (Sk + S::BKV - 1) / S::BKV;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt_idx = id % kvtiles;
+  const int bh = id / kvtiles;
+  const int hk = bh % Hk, b = bh / Hk;
+  const int kv0 = kt_idx * S::BKV;
+  const int off = Sk - Sq;  // key n visible to query i iff n <= i + off
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int kv0w = kv0 + 32 * wave;
+  const int my_kv = kv0w + lr;
+  const float scale_log2 = a.softmax_scale * kLog2e;
+
+  const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
+  const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
+
+  // ---- K tile -> LDS (wave w: blocks 8w .. 8w+7, rows 32w .. 32w+31)
+#pragma unroll
+  for (int ii = 0; ii < 8; ++ii) {
+    const int blk = 8 * wave + ii;
+    const int r = 4 * blk + (lane >> 4);
+    const int c = (lane & 15) ^ swz_chunk(r);
+    const int n = min(kv0 + r, Sk - 1);
+    load_lds16(kg + (int64_t)n * a.k_stride[1] + 8 * c, Ks + blk * 1024);
+  }
+  // ---- V rows of this wave (B operand of dP = dO Vᵀ)
+  u32x4 vB[D / 16];
+  {
+    const uint16_t* vp = vg + (int64_t)min(my_kv, Sk - 1) * a.v_stride[1];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) vB[c] = ld16(vp + 16 * c + 8 * lh);
+  }
+
+  // ---- per-lane LDS offsets
+  const int sw_lr = swz_chunk(lr);
+  auto rm_off = [&](int c) { return lr * S::ROWB + 16 * ((2 * c + lh) ^ sw_lr); };
+  // Transpose-read offset of rows 16k + r (r = 4(lane/32) + (lane%16)/4, +8
+  // for hf = 1), columns 32dt + 16((lane/16)%2) + 4(lane%4) of a 256 B-row tile.
+  const int tr_r0 = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_q = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int tr_b = 8 * (lane & 1);
+  auto toff = [&](int hf, int dt) {
+    const int r = tr_r0 + 8 * hf;
+    return r * S::ROWB + 16 * ((4 * dt + tr_q) ^ swz_chunk(r)) + tr_b;
+  };
+  // dSᵀ transpose reads: rows 16kc + r, piece 4((k/16)%2) + k%4.
+  const int ds_r = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int ds_p = 4 * ((lane >> 4) & 1) + (lane & 3);
+
+  f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
+
+  const int q_begin = CAUSAL ? max(0, kv0 - off) : 0;
+  const int it0 = q_begin / S::BQ;
+  const int it1 = (Sq + S::BQ - 1) / S::BQ;
+  const int nit = max(it1 - it0, 0);
+  const int ntot = nit * G;
+  const int wkv_last = min(kv0w + 31, Sk - 1);
+
+  // Iteration t: query head hk*G + t / nit, query tile it0 + t % nit.
+  auto issue_q = [&](int t, char* qb, char* ob, float* st) {
+    const int h = hk * G + t / nit;
+    const int i0 = (it0 + t % nit) * S::BQ;
+    const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] + h * a.q_stride[2];
+    const uint16_t* og = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
+                         h * a.do_stride[2];
+    const int r = 4 * wave + (lane >> 4);
+    const int c = (lane & 15) ^ swz_chunk(r);
+    const int i = min(i0 + r, Sq - 1);
+    load_lds16(qg + (int64_t)i * a.q_stride[1] + 8 * c, qb + wave * 1024);
+    load_lds16(og + (int64_t)i * a.do_stride[1] + 8 * c, ob + wave * 1024);
+    if (wave == 0) {
+      const int64_t stat0 = ((int64_t)b * H + h) * Sq;
+      const int ii = min(i0 + (lane & 31), Sq - 1);
+      const float* src = (lane < 32) ? lse2 + stat0 + ii : rowdot + stat0 + ii;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)st, 4, 0, 0);
+    }
+  };
+
+  auto step = [&](int t, const char* qb, const char* ob, const float* st) {
+    const int h = hk * G + t / nit;
+    const int i0 = (it0 + t % nit) * S::BQ;
+    const bool active = (!CAUSAL || (i0 + S::BQ - 1 + off >= kv0w)) && kv0w < Sk;
+    if (active) {
+      f32x16 s, dp;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        const u32x4 aq = ld16(qb + rm_off(c));
+        const u32x4 bk = ld16(Ks + 32 * wave * S::ROWB + rm_off(c));
+        const u32x4 ao = ld16(ob + rm_off(c));
+        s = T::mma32(aq, bk, s);
+        dp = T::mma32(ao, vB[c], dp);
+      }
+      // s[i], dp[i]: query i0 + 8(i/4) + 4lh + (i%4), key my_kv.
+      const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kv0w + 32 > Sk) ||
+                             (i0 + S::BQ > Sq);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int qb4 = 8 * g + 4 * lh;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + qb4);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + S::BQ + qb4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 4 * g + r;
+          float p = fast_exp2(fmaf(s[i], scale_log2, -l4[r]));
+          if (need_mask) {
+            const int qi = i0 + qb4 + r;
+            const bool vis = (my_kv < Sk) && (qi < Sq) && (!CAUSAL || my_kv <= qi + off);
+            p = vis ? p : 0.f;
+          }
+          s[i] = p;
+          dp[i] = p * (dp[i] - d4[r]);
+        }
+      }
+      u32x4 pB[2], sB[2];
+#pragma unroll
+      for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int e = 8 * kq + 2 * w;
+          pB[kq][w] = T::pack(s[e], s[e + 1]);
+          sB[kq][w] = T::pack(dp[e], dp[e + 1]);
+        }
+      // dSᵀ row my_kv - kv0 = 32w + lr; queries 8g + 4lh .. +3 = piece 2g + lh.
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int kq = g >> 1, w0 = 2 * (g & 1);
+        const u32x2 v = {sB[kq][w0], sB[kq][w0 + 1]};
+        st8(dSt + ds_piece(32 * wave + lr, 2 * g + lh), v);
+      }
+      // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads)
+#pragma unroll
+      for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const int ro = kq * 16 * S::ROWB;
+          const u32x2 o_lo = lds_read_tr(ob + toff(0, dt) + ro);
+          const u32x2 o_hi = lds_read_tr(ob + toff(1, dt) + ro);
+          const u32x2 q_lo = lds_read_tr(qb + toff(0, dt) + ro);
+          const u32x2 q_hi = lds_read_tr(qb + toff(1, dt) + ro);
+          const u32x4 ao = {o_lo[0], o_lo[1], o_hi[0], o_hi[1]};
+          const u32x4 aq = {q_lo[0], q_lo[1], q_hi[0], q_hi[1]};
+          dv[dt] = T::mma32(ao, pB[kq], dv[dt]);
+          dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
+        }
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) st8(dSt + ds_piece(32 * wave + lr, 2 * g + lh), u32x2{0, 0});
+    }
+    __syncthreads();  // dSᵀ complete
+
+    // dQ[i0 + q][32w + d] += sum over the 256 keys, waves 0..3 (one 32-wide d tile each).
+    const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
+    if (wave < 4 && any) {
+      const int dt = wave;
+      f32x16 acc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < S::BKV / 16; ++kc) {
+        const int par = 4 * (kc & 1);
+        const u32x2 s_lo = lds_read_tr(dSt + (16 * kc + ds_r) * S::DS_ROWB +
+                                       8 * (ds_p ^ ((ds_r >> 2) + par)));
+        const u32x2 s_hi = lds_read_tr(dSt + (16 * kc + ds_r + 8) * S::DS_ROWB +
+                                       8 * (ds_p ^ (((ds_r + 8) >> 2) + par)));
+        const int ro = kc * 16 * S::ROWB;
+        const u32x2 k_lo = lds_read_tr(Ks + toff(0, dt) + ro);
+        const u32x2 k_hi = lds_read_tr(Ks + toff(1, dt) + ro);
+        const u32x4 as = {s_lo[0], s_lo[1], s_hi[0], s_hi[1]};
+        const u32x4 bk = {k_lo[0], k_lo[1], k_hi[0], k_hi[1]};
+        acc = T::mma32(as, bk, acc);
+      }
+      // acc[4g + r] = dQ[query i0 + 8g + 4lh + r][d 32dt + lr]; dqacc is
+      // [B, H, Sq, D], so row r of group g is an immediate offset r*D.
+      float* dqh = dqacc + (((int64_t)b * H + h) * Sq + i0 + 4 * lh) * D + 32 * dt + lr;
+      if (i0 + S::BQ <= Sq) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float* pg = dqh + 8 * g * D;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) unsafeAtomicAdd(pg + r * D, acc[4 * g + r]);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (i0 + 8 * g + 4 * lh + r < Sq) unsafeAtomicAdd(dqh + (8 * g + r) * D, acc[4 * g + r]);
+      }
+    }
+  };
+
+  if (ntot > 0) issue_q(0, Q0, O0, st0);
+  for (int t = 0; t < ntot; t += 2) {
+    wait_vmem();
+    __syncthreads();  // tile t (and K on the first pass) resident; dSᵀ free
+    if (t + 1 < ntot) issue_q(t + 1, Q1, O1, st1);
+    step(t, Q0, O0, st0);
+    if (t + 1 >= ntot) break;
+    wait_vmem();
+    __syncthreads();
+    if (t + 2 < ntot) issue_q(t + 2, Q0, O0, st0);
+    step(t + 1, Q1, O1, st1);
+  }
+  wait_vmem();
+
+  if (my_kv < Sk) {
+    uint16_t* dkp = static_cast<uint16_t*>(a.dk) + b * a.dk_stride[0] +
+                    (int64_t)my_kv * a.dk_stride[1] + hk * a.dk_stride[2];
+    uint16_t* dvp = static_cast<uint16_t*>(a.dv) + b * a.dv_stride[0] +
+                    (int64_t)my_kv * a.dv_stride[1] + hk * a.dv_stride[2];
+    const float sc = a.softmax_scale;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * dt + 8 * g + 4 * lh;
+        u32x2 wk, wv;
+        wk[0] = T::pack(dk[dt][4 * g] * sc, dk[dt][4 * g + 1] * sc);
+        wk[1] = T::pack(dk[dt][4 * g + 2] * sc, dk[dt][4 * g + 3] * sc);
+        wv[0] = T::pack(dv[dt][4 * g], dv[dt][4 * g + 1]);
+        wv[1] = T::pack(dv[dt][4 * g + 2], dv[dt][4 * g + 3]);
+        st8(dkp + d, wk);
+        st8(dvp + d, wv);
+      }
+  }
+}
+
+}  // namespace fa
