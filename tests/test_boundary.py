@@ -176,7 +176,7 @@ def decode_args(**over):
 def test_decode_workspace_and_checks():
     lib = _lib.load()
     a = decode_args()
-    rows = 64 * 32 * (32768 // 256)
+    rows = 64 * 32 * (32768 // 512)  # D=128, page >= 16: 512-key splits
     assert lib.fa_decode_workspace_bytes(ctypes.byref(a)) == rows * 128 * 4 + rows * 4 + 256
     assert lib.fa_paged_decode(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE
     assert lib.fa_paged_decode(ctypes.byref(decode_args(max_seq_len=100)), 0x6000, 1 << 40,

@@ -17,7 +17,10 @@
 //     combine kernel merges chunks with LSE weights (the online-softmax merge
 //     of the dormant split variant, _kernels_paged.py:175-187).
 // The decode mask is `key < seq_len` (_kernels_paged.py:450-451).
+#include <algorithm>
+
 #include "fa_common.h"
+#include "fa_decode_stream.h"
 #include "fa_internal.h"
 
 namespace fa {
@@ -53,6 +56,7 @@ struct DecodeWs {
   float* po;    // [B, Hq, nsplit, D]   normalised partial outputs
   float* plse;  // [B, Hq, nsplit]      base-2 log-sum-exp of each chunk
   int nsplit;
+  int split;    // keys per split
 };
 
 template <class T, int D, int GB>
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(fa_decode_args a,
 template <class T, int D>
 __global__ __launch_bounds__(64) void decode_combine_kernel(fa_decode_args a,
                                                             DecodeWs ws) {
-  constexpr int CH = dec_chunk(D);
+  const int CH = ws.split;
   constexpr int NP = (D + 127) / 128;  // d pairs per lane: 2*lane + 128*k
   __shared__ float wts[64];
   const int hq = blockIdx.x % a.num_heads;
@@ -271,11 +275,6 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(fa_decode_args a,
 
 // ----------------------------------------------------------------- launchers
 
-int decode_num_splits(const fa_decode_args& a) {
-  const int ch = dec_chunk(a.head_dim);
-  return (a.max_seq_len + ch - 1) / ch;
-}
-
 int decode_group_size(const fa_decode_args& a) {
   const int G = a.num_heads / a.num_kv_heads;
   if (G % 8 == 0) return 8;
@@ -284,25 +283,80 @@ int decode_group_size(const fa_decode_args& a) {
   return 1;
 }
 
+// The streaming kernel (fa_decode_stream.h) covers head_dim 128 with pages of
+// at least 16 keys, at most kMaxGroup query heads per item, and token strides
+// whose 16-row offsets fit its 32-bit lane offsets; other shapes use
+// decode_split_kernel.
+static bool use_stream(const fa_decode_args& a) {
+  const int64_t lim = int64_t(1) << 26;
+  return a.head_dim == 128 && a.page_size >= 16 && a.batch <= DecStream::kMaxBatch &&
+         decode_group_size(a) <= DecStream::kMaxGroup && a.k_stride[1] >= 0 &&
+         a.k_stride[1] < lim && a.v_stride[1] >= 0 && a.v_stride[1] < lim;
+}
+
+static int decode_split_size(const fa_decode_args& a) {
+  return use_stream(a) ? DecStream::kSplit : dec_chunk(a.head_dim);
+}
+
+int decode_num_splits(const fa_decode_args& a) {
+  const int ch = decode_split_size(a);
+  return (a.max_seq_len + ch - 1) / ch;
+}
+
+
 size_t decode_workspace_bytes(const fa_decode_args& a) {
   const size_t rows = (size_t)a.batch * a.num_heads * (size_t)decode_num_splits(a);
   return rows * (size_t)a.head_dim * sizeof(float) + rows * sizeof(float) + 256;
+}
+
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <class T, int D>
+static hipError_t launch_combine(const fa_decode_args& a, DecodeWs ws, hipStream_t st) {
+  hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.batch * a.num_heads)),
+                     dim3(64), 0, st, a, ws);
+  return hipGetLastError();
 }
 
 template <class T, int D, int GB>
 static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
                                    hipStream_t st) {
   const int G = a.num_heads / a.num_kv_heads;
-  const int64_t nblk = (int64_t)ws.nsplit * (G / GB) * a.num_kv_heads * a.batch;
-  if (nblk > 0) {  // max_seq_len == 0: the combine alone writes zeros
-    hipLaunchKernelGGL((decode_split_kernel<T, D, GB>), dim3((unsigned)nblk), dim3(256), 0, st,
+  const int64_t items = (int64_t)ws.nsplit * (G / GB) * a.num_kv_heads * a.batch;
+  if (items > 0) {  // max_seq_len == 0: the combine alone writes zeros
+    if constexpr (D == 128) {
+      if (use_stream(a)) {
+        const int64_t wgs = std::max<int64_t>(
+            1, std::min<int64_t>((items + DecStream::kWavesPerWG - 1) / DecStream::kWavesPerWG,
+                                 (int64_t)device_cu_count() * DecStream::kWavesPerCU /
+                                     DecStream::kWavesPerWG));
+        DecodeWsS wss{ws.po, ws.plse, ws.nsplit};
+        hipLaunchKernelGGL((decode_stream_kernel<T, GB>), dim3((unsigned)wgs),
+                           dim3(64 * DecStream::kWavesPerWG), 0,
+                           st, a, wss);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_combine<T, D>(a, ws, st);
+      }
+    }
+    hipLaunchKernelGGL((decode_split_kernel<T, D, GB>), dim3((unsigned)items), dim3(256), 0, st,
                        a, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.batch * a.num_heads)),
-                     dim3(64), 0, st, a, ws);
-  return hipGetLastError();
+  return launch_combine<T, D>(a, ws, st);
 }
 
 template <class T, int D>
@@ -328,6 +382,7 @@ static hipError_t launch_decode_t(const fa_decode_args& a, DecodeWs ws, hipStrea
 hipError_t launch_decode(const fa_decode_args& a, void* workspace, hipStream_t st) {
   DecodeWs ws;
   ws.nsplit = decode_num_splits(a);
+  ws.split = decode_split_size(a);
   const size_t rows = (size_t)a.batch * a.num_heads * (size_t)ws.nsplit;
   char* base = static_cast<char*>(workspace);
   ws.po = reinterpret_cast<float*>(base);
