@@ -1,6 +1,7 @@
 """Benchmark of the MI355X attention path (one GPU).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-extra] [--no-cpu]
+python bench.py --calibrate-copy      (256 MiB copies, for counter calibration)
 
 Headline (`value`): BASELINE.json configs[1] — dense causal FlashAttention
 forward + backward, fp16, q/k/v/dO [B=4, S=2048, H=16, D=128], one step =
@@ -10,9 +11,13 @@ only: fwd 4*D*H*pairs, bwd 2.5x fwd).
 
 `roofline` covers the dominant launch of that step, the fa_bwd call (its
 pre / main / dQ-convert kernels), timed with HIP events on the stream it is
-launched on.  `extra` reports the other BASELINE configs and the north-star
-points (T1: S=8192 fwd+bwd, T2: decode at 32k context) with their own
-roofline fractions; paged/decode reps flush the 256 MB Infinity Cache.
+launched on; its `traffic` (HBM bytes per launch) comes from the counter
+runs summarised in profiles/fa_bwd_c2_traffic.md.  `extra` reports the other
+BASELINE configs and the north-star points (T1: S=8192 fwd+bwd, T2: decode
+at 32k context) with their own roofline fractions; paged/decode reps flush
+the 256 MB Infinity Cache.  Each entry's `ms` is GPU time per call (a spin
+kernel ahead of the start event hides the Python wrapper), `api_ms` the
+same interval without it, i.e. including host time the GPU spends idle.
 `cpu_baseline` times the CPU oracle (fp32 PyTorch math, the reference math
 path) on a bounded sample of the same workload on this host's cores.
 """
@@ -120,40 +125,93 @@ class CacheFlush:
         self.buf.fill_(1)
 
 
+_SLEEP_CYCLES = None
+
+
+def _sleep_cycles(target_ms=1.0):
+    """Argument of torch.cuda._sleep that keeps the GPU busy for ~target_ms."""
+    global _SLEEP_CYCLES
+    if _SLEEP_CYCLES is None:
+        n = 1 << 20
+        torch.cuda._sleep(n)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        torch.cuda._sleep(n)
+        e.record()
+        e.synchronize()
+        _SLEEP_CYCLES = max(1, int(n * target_ms / max(s.elapsed_time(e), 1e-3)))
+    return _SLEEP_CYCLES
+
+
 def time_reps(fn, reps, warmup, flush=None):
-    """Median per-call time (ms) from HIP events around each call."""
+    """Median per-call times (ms): (gpu, api).
+
+    gpu: a spin kernel queued ahead of the start event keeps the GPU busy
+    while Python prepares the call, so the interval holds only the GPU work
+    the call enqueues.  api: the same without the spin kernel, so host time
+    during which the GPU idles is included (the cost a caller sees).
+    """
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    times = []
-    for _ in range(reps):
-        if flush is not None:
-            flush()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        fn()
-        e.record()
-        e.synchronize()
-        times.append(s.elapsed_time(e))
-    return statistics.median(times), times
+    out = []
+    for hide_host in (True, False):
+        times = []
+        for _ in range(reps):
+            if flush is not None:
+                flush()
+            if hide_host:
+                torch.cuda._sleep(_sleep_cycles())
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            times.append(s.elapsed_time(e))
+        out.append(statistics.median(times))
+    return out[0], out[1]
 
 
-def flop_entry(name, flops, ms, extra=None):
+def flop_entry(name, flops, ms, api_ms=None, extra=None):
     tf = flops / (ms * 1e-3) / 1e12
     d = {"ms": round(ms, 4), "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
          "frac_of_peak": round(tf / PEAK_TFLOPS, 4)}
+    if api_ms is not None:
+        d["api_ms"] = round(api_ms, 4)
     if extra:
         d.update(extra)
     return name, d
 
 
-def bytes_entry(name, nbytes, ms, extra=None):
+def bytes_entry(name, nbytes, ms, api_ms=None, extra=None):
     gbs = nbytes / (ms * 1e-3) / 1e9
     d = {"ms": round(ms, 4), "gbytes": round(nbytes / 1e9, 3), "gbs": round(gbs, 1),
          "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    if api_ms is not None:
+        d["api_ms"] = round(api_ms, 4)
+        d["api_gbs"] = round(nbytes / (api_ms * 1e-3) / 1e9, 1)
     if extra:
         d.update(extra)
     return name, d
+
+
+def profiled_traffic(name):
+    """HBM bytes per launch recorded by the counter runs in profiles/<name>_traffic.md.
+
+    The summary holds a line `traffic_bytes_per_launch: N` (FETCH_SIZE and
+    WRITE_SIZE per dispatch, scaled by the copy-kernel calibration it
+    states).  None when no summary has been recorded.
+    """
+    path = os.path.join(REPO, "profiles", f"{name}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 # --------------------------------------------------------------------- legs
@@ -169,6 +227,7 @@ def headline(fa, steps, warmup, dev):
     f_step = 3.5 * f_fwd
 
     def step():
+        q.grad = k.grad = v.grad = None  # fresh gradients: the step is fwd + bwd only
         out = fa.tilelang_flash_attn_func(q, k, v, causal=True)
         out.backward(do)
 
@@ -197,14 +256,17 @@ def headline(fa, steps, warmup, dev):
     def bwd():
         _lib.check(lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), nbytes, stream), "fa_bwd")
 
-    bwd_ms, _ = time_reps(bwd, max(steps, 20), 3)
-    fwd_ms, _ = time_reps(lambda: _dense.forward(qd, kd, vd, D ** -0.5, True), max(steps, 20), 3)
+    bwd_ms, bwd_api = time_reps(bwd, max(steps, 20), 3)
+    fwd_ms, fwd_api = time_reps(lambda: _dense.forward(qd, kd, vd, D ** -0.5, True),
+                                max(steps, 20), 3)
     bwd_tf = 2.5 * f_fwd / (bwd_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(bwd_tf, 1), "peak": PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(bwd_tf / PEAK_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(bwd_tf / PEAK_TFLOPS, 4),
+                "traffic": profiled_traffic("fa_bwd_c2"),
                 "kernel": "fa_bwd (bwd_pre + bwd_main + bwd_dq_convert)",
                 "launch_ms": round(bwd_ms, 4), "algorithmic_gflop": round(2.5 * f_fwd / 1e9, 2)}
-    parts = dict([flop_entry("C2_fwd", f_fwd, fwd_ms), flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms)])
+    parts = dict([flop_entry("C2_fwd", f_fwd, fwd_ms, fwd_api),
+                  flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms, bwd_api)])
     return ms, f_step, roofline, parts
 
 
@@ -213,8 +275,8 @@ def extras(fa, dev, reps):
     flush = CacheFlush(dev)
     # C1: dense non-causal forward fp16 [1,512,16,64]
     q, k, v = dense_inputs(1, 512, 16, 64, torch.float16, dev, with_do=False)
-    ms, _ = time_reps(lambda: fa.tilelang_flash_attn_func(q, k, v), reps, 5)
-    res.update([flop_entry("C1_fwd", 4 * 64 * 16 * 512 * 512, ms)])
+    ms, api = time_reps(lambda: fa.tilelang_flash_attn_func(q, k, v), reps, 5)
+    res.update([flop_entry("C1_fwd", 4 * 64 * 16 * 512 * 512, ms, api)])
 
     # T1: dense causal fwd+bwd S=8192 D=128, B=2 H=16
     q, k, v, do = dense_inputs(2, 8192, 16, 128, torch.float16, dev)
@@ -223,14 +285,15 @@ def extras(fa, dev, reps):
     f_fwd = 4 * 128 * 16 * dense_pairs(8192, 8192, True) * 2
 
     def t1():
+        q.grad = k.grad = v.grad = None
         o = fa.tilelang_flash_attn_func(q, k, v, causal=True)
         o.backward(do)
 
-    ms, _ = time_reps(t1, max(reps // 2, 5), 2)
-    res.update([flop_entry("T1_fwd_bwd", 3.5 * f_fwd, ms)])
-    ms, _ = time_reps(lambda: fa.tilelang_flash_attn_func(q.detach(), k.detach(), v.detach(),
+    ms, api = time_reps(t1, max(reps // 2, 5), 2)
+    res.update([flop_entry("T1_fwd_bwd", 3.5 * f_fwd, ms, api)])
+    ms, api = time_reps(lambda: fa.tilelang_flash_attn_func(q.detach(), k.detach(), v.detach(),
                                                           causal=True), reps, 3)
-    res.update([flop_entry("T1_fwd", f_fwd, ms)])
+    res.update([flop_entry("T1_fwd", f_fwd, ms, api)])
     del q, k, v, do
 
     # C3: paged causal prefill fp16, 8 seqs U[512,4096], 32/8 heads, D=128
@@ -238,8 +301,8 @@ def extras(fa, dev, reps):
     c = paged_inputs(lens, lens, [0] * 8, 32, 8, 128, torch.float16, dev, g)
     pairs = sum(n * (n + 1) // 2 for n in lens)
     run = lambda: fa.tilelang_paged_forward(**c)  # noqa: E731
-    ms, _ = time_reps(run, reps, 3, flush)
-    res.update([flop_entry("C3_paged_prefill", 4 * 128 * 32 * pairs, ms)])
+    ms, api = time_reps(run, reps, 3, flush)
+    res.update([flop_entry("C3_paged_prefill", 4 * 128 * 32 * pairs, ms, api)])
     del c
 
     # C5: chunked prefill with prefix, bf16, 16 x 512 new tokens, 64/8 heads
@@ -247,8 +310,8 @@ def extras(fa, dev, reps):
     c = paged_inputs([512] * 16, [p + 512 for p in pf], pf, 64, 8, 128, torch.bfloat16, dev, g)
     pairs = sum(sum(min(p + t + 1, p + 512) for t in range(512)) for p in pf)
     run = lambda: fa.tilelang_paged_forward(**c)  # noqa: E731
-    ms, _ = time_reps(run, reps, 3, flush)
-    res.update([flop_entry("C5_chunked_prefill_bf16", 4 * 128 * 64 * pairs, ms)])
+    ms, api = time_reps(run, reps, 3, flush)
+    res.update([flop_entry("C5_chunked_prefill_bf16", 4 * 128 * 64 * pairs, ms, api)])
     del c
 
     # C4 / T2: paged decode, batch 64, 32/8 heads, D=128
@@ -260,8 +323,8 @@ def extras(fa, dev, reps):
         qd = c["q"].view(64, 32, 128)
         run = lambda: fa.tilelang_decode_forward(qd, c["k_cache"], c["v_cache"],  # noqa: E731
                                                  c["block_table"], c["seq_lens"])
-        ms, _ = time_reps(run, reps, 3, flush)
-        res.update([bytes_entry(name, decode_bytes(lens, 32, 8, 128), ms)])
+        ms, api = time_reps(run, reps, 3, flush)
+        res.update([bytes_entry(name, decode_bytes(lens, 32, 8, 128), ms, api)])
         del c, qd
     return res
 
@@ -298,6 +361,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 device copies of 256 MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -306,9 +371,19 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    import tilelang_fa_v100 as fa
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        # A plain copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of
+        # this kernel against 256 MiB give the counters' scale factors.
+        x = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": 256 << 20, "dispatches": 5}), flush=True)
+        return
+    import tilelang_fa_v100 as fa
     print(f"[bench] headline C2: warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
     ms, f_step, roof, parts = headline(fa, args.steps, args.warmup, dev)
     extra = dict(parts)

@@ -226,8 +226,8 @@ static int check_decode(const fa_decode_args* a) {
   if (!strides_ok(a->q_stride, 2) || !strides_ok(a->k_stride, 3) || !strides_ok(a->v_stride, 3) ||
       a->o_stride[0] < 0 || a->o_stride[1] < 0)
     return fail(FA_E_UNSUPPORTED, "fa_paged_decode: unsupported strides");
-  const int64_t chunk = 32768 / a->head_dim;  // keys per decode split
-  const int64_t nsplit = (a->max_seq_len + chunk - 1) / chunk;
+  // Work items and partial rows are counted in int on the device.
+  const int64_t nsplit = fa::decode_num_splits(*a);
   if (nsplit * a->num_heads * a->batch > kIntMax)
     return fail(FA_E_UNSUPPORTED, "fa_paged_decode: problem too large");
   return ok();

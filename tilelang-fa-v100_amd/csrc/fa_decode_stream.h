@@ -252,11 +252,14 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   const uint32_t ring_base = lds_addr(ring[wv][0]);
   const uint32_t q_base = lds_addr(qslot[wv][0]);
 
-  // ---- producer: issues the loads of tile (pI, pt) into ring slot `slot`:
-  // 8 DMA instructions, 4 rows of 256 bytes each.  Every call issues them
-  // (after the last tile it reloads that tile), which the fixed vmcnt in
-  // lds_read_tile relies on.  The page index of the next tile is read
-  // (scalar load) one call early.
+  // ---- producer.  prepare() computes the addresses of tile (pI, pt) and
+  // advances to the next tile; issue(slot) then puts its 8 DMA instructions
+  // (4 rows of 256 bytes each) into ring slot `slot`.  The split lets the
+  // address work run before the wait for the tile being replaced, so only
+  // the DMA issue separates that tile's arrival from the refill.  Every
+  // issue() emits the 8 instructions (after the last tile it reloads that
+  // tile), which the fixed vmcnt in lds_read_tile relies on.  The page index
+  // of a tile is read (scalar load) one prepare() early.
   int pI = I0, pt = 0;
   DecItem pit = dec_item(pI, pfx, seq_lens, cap, B, HG, ngroups);
   bool pdone = false;
@@ -268,48 +271,28 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   // Query slot: holds the rows of item q_item (-1: free).  Rows past GB
   // repeat row GB - 1 so that every DMA instruction stays in bounds.
   int q_item = -1;
-  auto dma_q = [&](const DecItem& it) {
-    const int h0 = it.hk * G + it.hg * GB;
-    const uint16_t* q0 = static_cast<const uint16_t*>(a.q) + (int64_t)it.b * a.q_stride[0];
-#pragma unroll
-    for (int r0 = 0; r0 < QR; r0 += 4)
-      ld16_lds_nt(q0 + (int64_t)(h0 + min(r0 + grp, GB - 1)) * a.q_stride[1] + 8 * l16,
-                  qslot[wv][r0]);
-  };
-  auto produce = [&](int slot) {
+  // Prepared tile: base rows of K and V, number of valid rows - 1 (15 for a
+  // full tile) and the query rows to fetch with it (q_src, or none).
+  const uint16_t* kc_n = nullptr;
+  const uint16_t* vc_n = nullptr;
+  int dr_n = TK - 1;
+  const uint16_t* q_src = nullptr;
+  int q_h0 = 0;
+  auto prepare = [&]() {
+    q_src = nullptr;
     if (pt == 0 && q_item < 0 && !pdone) {
-      dma_q(pit);
+      q_src = static_cast<const uint16_t*>(a.q) + (int64_t)pit.b * a.q_stride[0];
+      q_h0 = pit.hk * G + pit.hg * GB;
       q_item = pI;
     }
     const int n = pit.n_begin + pt * TK;  // first key of the tile
-    const int last = pit.n_end - 1;
+    dr_n = min(TK - 1, pit.n_end - 1 - n);
     const int64_t page = min((unsigned)page_next, last_page);
     const int tok0 = n & ps_mask;  // tiles are 16-aligned and never cross a page
-    const uint16_t* kc = static_cast<const uint16_t*>(a.k_cache) + (int64_t)pit.hk * a.k_stride[2] +
-                         page * a.k_stride[0] + (int64_t)tok0 * ks1;
-    const uint16_t* vc = static_cast<const uint16_t*>(a.v_cache) + (int64_t)pit.hk * a.v_stride[2] +
-                         page * a.v_stride[0] + (int64_t)tok0 * vs1;
-    char* kb = ring[wv][slot];
-    char* vb = kb + TK * RB;
-    if (n + TK - 1 <= last) {
-#pragma unroll
-      for (int c = 0; c < TK / 4; ++c) {
-        ld16_lds_nt(kc + kdma[c], kb + 1024 * c);
-        ld16_lds_nt(vc + vdma[c], vb + 1024 * c);
-      }
-    } else {  // last tile of the item: rows past its end repeat the last key
-#pragma unroll
-      for (int c = 0; c < TK / 4; ++c) {
-        const int r = 4 * c + grp;
-        const int dr = min(n + r, last) - n;
-        const int j = 8 * (l16 ^ dec_swz(r));
-        ld16_lds_nt(kc + dr * ks1 + j, kb + 1024 * c);
-        ld16_lds_nt(vc + dr * vs1 + j, vb + 1024 * c);
-      }
-    }
-    // Keeps the next call's DMA behind this one in issue order (the slots are
-    // distinct memory, so the compiler could otherwise interleave them).
-    asm volatile("" ::: "memory");
+    kc_n = static_cast<const uint16_t*>(a.k_cache) + (int64_t)pit.hk * a.k_stride[2] +
+           page * a.k_stride[0] + (int64_t)tok0 * ks1;
+    vc_n = static_cast<const uint16_t*>(a.v_cache) + (int64_t)pit.hk * a.v_stride[2] +
+           page * a.v_stride[0] + (int64_t)tok0 * vs1;
     if (pdone) return;
     if (pt + 1 < pit.ntiles) {
       ++pt;
@@ -321,6 +304,35 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
       return;
     }
     page_next = page_of(pit, pt);
+  };
+  auto issue = [&](int slot) {
+    if (q_src) {
+#pragma unroll
+      for (int r0 = 0; r0 < QR; r0 += 4)
+        ld16_lds_nt(q_src + (int64_t)(q_h0 + min(r0 + grp, GB - 1)) * a.q_stride[1] + 8 * l16,
+                    qslot[wv][r0]);
+    }
+    char* kb = ring[wv][slot];
+    char* vb = kb + TK * RB;
+    if (dr_n == TK - 1) {
+#pragma unroll
+      for (int c = 0; c < TK / 4; ++c) {
+        ld16_lds_nt(kc_n + kdma[c], kb + 1024 * c);
+        ld16_lds_nt(vc_n + vdma[c], vb + 1024 * c);
+      }
+    } else {  // last tile of the item: rows past its end repeat the last key
+#pragma unroll
+      for (int c = 0; c < TK / 4; ++c) {
+        const int r = 4 * c + grp;
+        const int dr = min(r, dr_n);
+        const int j = 8 * (l16 ^ dec_swz(r));
+        ld16_lds_nt(kc_n + dr * ks1 + j, kb + 1024 * c);
+        ld16_lds_nt(vc_n + dr * vs1 + j, vb + 1024 * c);
+      }
+    }
+    // Keeps the next call's DMA behind this one in issue order (the slots are
+    // distinct memory, so the compiler could otherwise interleave them).
+    asm volatile("" ::: "memory");
   };
 
   // ---- consumer state.  S^T and O^T use the 16x16x32 layout: lane
@@ -416,19 +428,26 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
     }
   };
 
-  // ---- pipeline: a step reads the tile in ring slot s into registers,
-  // refills the slot with the tile PD ahead and then computes, so PD tiles
+  // ---- pipeline: a step prepares the tile PD ahead, reads the tile in ring
+  // slot s into registers, refills the slot and then computes, so PD tiles
   // are in flight during the compute.  The loop leaves only after a whole
   // group of PD steps; loads past the last tile only reload it.
 #pragma unroll
-  for (int s = 0; s < PD; ++s) produce(s);
+  for (int s = 0; s < PD; ++s) {
+    prepare();
+    issue(s);
+  }
   do {
 #pragma unroll
     for (int s = 0; s < PD; ++s) {
       u32x4 kr[D / 32];
       u32x2 vt[D / 16];
+      prepare();
+      // Pins the prepared addresses ahead of the wait (volatile asm keeps its
+      // order; the compiler would otherwise sink the address work past it).
+      asm volatile("" ::"s"(kc_n), "s"(vc_n), "s"(dr_n), "s"(q_src));
       lds_read_tile(ring_base + s * S::kTileBytes, koff, voff, kr, vt);
-      produce(s);
+      issue(s);
       if (cI < I1) consume(kr, vt);
     }
   } while (cI < I1);
