@@ -13,7 +13,10 @@
 //
 // Kernels:
 //   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row; zeroes
-//                       the dQ accumulator rows it covers.
+//                       the dQ accumulator rows it covers.  Both statistics
+//                       live in one array [B*H][2][Sq] (LSE*log2(e) first,
+//                       rowdot second), so a lane addresses either with a
+//                       32-bit offset from a per-head base.
 //   bwd_main_kernel     workgroup = 128 keys (32 per wave) of one KV head;
 //                       loops over the 64-row query tiles of every query
 //                       head that shares the KV head (GQA).  K and V of the wave stay in registers,
@@ -52,7 +55,7 @@ struct BwdShape {
 // ------------------------------------------------------------ preprocess
 template <class T, int D>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqacc,
-                                                      float* rowdot, float* lse2) {
+                                                      float* stats) {
   constexpr int LPR = D / 8;          // lanes per row
   constexpr int RPB = 256 / LPR;      // rows per block
   const int64_t nrows = (int64_t)a.batch * a.seqlen_q * a.num_heads;
@@ -80,19 +83,19 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 #pragma unroll
   for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
   if (r < nrows && sub == 0) {
-    const int64_t idx = ((int64_t)b * a.num_heads + h) * a.seqlen_q + q;
-    rowdot[idx] = acc;
-    const float l = a.lse[idx];
+    const int64_t bh = (int64_t)b * a.num_heads + h;
+    const float l = a.lse[bh * a.seqlen_q + q];
+    float* st = stats + 2 * bh * a.seqlen_q + q;
     // A row that saw no key has lse = -inf; +inf makes its P exactly zero.
-    lse2[idx] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
+    st[0] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
+    st[a.seqlen_q] = acc;
   }
 }
 
 // ------------------------------------------------------------ main kernel
 template <class T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqacc,
-                                                       const float* rowdot,
-                                                       const float* lse2) {
+                                                       const float* stats) {
   using S = BwdShape<D>;
   __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
   __shared__ __attribute__((aligned(16))) float lse_s[S::BQ];
@@ -192,8 +195,8 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     }
     if (tid < S::BQ) {
       const int i = i0 + tid;
-      lreg = i < Sq ? lse2[stat0 + i] : __builtin_inff();
-      dreg = i < Sq ? rowdot[stat0 + i] : 0.f;
+      lreg = i < Sq ? stats[2 * stat0 + i] : __builtin_inff();
+      dreg = i < Sq ? stats[2 * stat0 + Sq + i] : 0.f;
     }
   };
   auto store_q = [&]() {
@@ -412,11 +415,10 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   using S = BwdShape<D>;
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
   float* dqacc = static_cast<float*>(ws);
-  float* rowdot = dqacc + rows * D;
-  float* lse2 = rowdot + rows;
+  float* stats = dqacc + rows * D;  // [B*H][2][Sq]
   constexpr int RPB = 256 / (D / 8);
   const dim3 rgrid((unsigned)((rows + RPB - 1) / RPB));
-  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, rowdot, lse2);
+  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if constexpr (D == 128) {
@@ -426,22 +428,20 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
     } else if (a.causal)
-      hipLaunchKernelGGL((bwd_main_d128_kernel<T, true>), grid, dim3(512), 0, st, a, dqacc,
-                         rowdot, lse2);
+      hipLaunchKernelGGL((bwd_main_d128_kernel<T, true>), grid, dim3(64 * S2::NW), 0, st, a,
+                         dqacc, stats);
     else
-      hipLaunchKernelGGL((bwd_main_d128_kernel<T, false>), grid, dim3(512), 0, st, a, dqacc,
-                         rowdot, lse2);
+      hipLaunchKernelGGL((bwd_main_d128_kernel<T, false>), grid, dim3(64 * S2::NW), 0, st, a,
+                         dqacc, stats);
   } else {
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
     } else if (a.causal)
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc,
-                         rowdot, lse2);
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc, stats);
     else
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc,
-                         rowdot, lse2);
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc, stats);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -2,11 +2,12 @@
 //
 // Same mathematics as bwd_main_kernel (fa_bwd.hip): per (key tile, query
 // tile) the 5 products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS and
-// dQ += dS K, with P = exp2(S·scale·log2e − lse2) and dS = P (dP − rowdot).
+// dQ += dS K, with P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot).
 // Layout, for the gfx950 memory instructions:
-//  * 8 waves x 32 keys = 256 keys per workgroup, so the fp32 atomics that
-//    reduce dQ across key tiles cover 256 keys each.
-//  * The workgroup's K tile (256 x 256 B) is copied once HBM -> LDS with
+//  * NW waves x 32 keys per workgroup (NW = 8: 256 keys), so the fp32
+//    atomics that reduce dQ across key tiles cover 256 keys each and every
+//    Q / dO tile fetched into LDS serves 256 keys.
+//  * The workgroup's K tile (128 x 256 B) is copied once HBM -> LDS with
 //    global_load_lds_dwordx4 and serves as the B operand of S (row reads)
 //    and of dQ (transpose reads).  V rows of each wave stay in registers.
 //  * Q and dO tiles (32 rows) are DMA'd the same way, double-buffered in
@@ -15,7 +16,9 @@
 //    in registers.
 //  * dSᵀ goes to LDS with 8-byte stores (its 8-byte pieces XOR-swizzled by
 //    row so both the stores and the transpose reads are conflict free) and
-//    is read back transposed as the A operand of dQ.
+//    is read back transposed as the A operand of dQ.  Each wave computes
+//    the 32 x 32 dQ block of one 32-wide d tile over all 128 keys and adds
+//    it to the fp32 accumulator with one atomic per element.
 //  * 256-byte K / Q / dO rows use the 16-byte-chunk swizzle of
 //    fa_fwd_d128.h.
 #pragma once
@@ -28,24 +31,21 @@ namespace fa {
 
 struct BwdShapeD128 {
   static constexpr int D = 128;
-  static constexpr int BKV = 256;  // keys per workgroup (32 per wave)
-  static constexpr int BQ = 32;    // query rows per iteration
+  static constexpr int NW = 8;        // waves per workgroup
+  static constexpr int BKV = 32 * NW; // keys per workgroup (32 per wave)
+  static constexpr int BQ = 32;       // query rows per iteration
   static constexpr int ROWB = 256;
   static constexpr int K_BYTES = BKV * ROWB;  // 64 KB
   static constexpr int QT_BYTES = BQ * ROWB;  // 8 KB
   static constexpr int DS_ROWB = BQ * 2;      // 64 B per dSᵀ row
   static constexpr int DS_BYTES = BKV * DS_ROWB;
+  static constexpr int DQW = D / 32;          // waves computing dQ (one d tile each)
+  static_assert(NW >= DQW && (8 % NW) == 0, "tile loader / dQ split");
 };
 
-// Byte offset of the 8-byte piece p (0..7) of dSᵀ row r.
-__device__ __forceinline__ int ds_piece(int r, int p) {
-  return r * BwdShapeD128::DS_ROWB + 8 * (p ^ ((r >> 2) & 7));
-}
-
 template <class T, bool CAUSAL>
-__global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc,
-                                                               const float* rowdot,
-                                                               const float* lse2) {
+__global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc,
+                                                               const float* stats) {
   using S = BwdShapeD128;
   constexpr int D = S::D;
   __shared__ __attribute__((aligned(16))) char Ks[S::K_BYTES];
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
   const int G = H / Hk;
   const int kvtiles = (Sk + S::BKV - 1) / S::BKV;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int kt_idx = id % kvtiles;
+  const int kt_idx = id % kvtiles;  // smallest key index first: most query rows
   const int bh = id / kvtiles;
   const int hk = bh % Hk, b = bh / Hk;
   const int kv0 = kt_idx * S::BKV;
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
 
-  // ---- K tile -> LDS (wave w: blocks 8w .. 8w+7, rows 32w .. 32w+31)
+  // ---- K tile -> LDS (wave w: 1 KB blocks 8w .. 8w+7 = rows 32w .. 32w+31)
 #pragma unroll
   for (int ii = 0; ii < 8; ++ii) {
     const int blk = 8 * wave + ii;
@@ -90,18 +90,36 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
     for (int c = 0; c < D / 16; ++c) vB[c] = ld16(vp + 16 * c + 8 * lh);
   }
 
-  // ---- per-lane LDS offsets
+  // ---- per-lane LDS offsets.  Chunk c of row r sits at chunk c ^ swz(r);
+  // the chunk-index bits a product walks (c for row reads, the 64-byte d
+  // tile for transpose reads) are free in the lane's base offset, so every
+  // offset is that base XOR an instruction constant (one register per
+  // pattern instead of one per chunk).
   const int sw_lr = swz_chunk(lr);
-  auto rm_off = [&](int c) { return lr * S::ROWB + 16 * ((2 * c + lh) ^ sw_lr); };
-  // Transpose-read offset of rows 16k + r (r = 4(lane/32) + (lane%16)/4, +8
-  // for hf = 1), columns 32dt + 16((lane/16)%2) + 4(lane%4) of a 256 B-row tile.
+  // Row read of chunk pair c (row lr, chunk 2c + lh):
+  // 16((2c + lh) ^ sw) = 32(c ^ (sw >> 1)) + 16(lh ^ (sw & 1)).
+  const int rm_base = lr * S::ROWB + 16 * (lh ^ (sw_lr & 1)) + 32 * (sw_lr >> 1);
+  int rb = rm_base;  // opaque per-iteration copy, see `step`
+  auto rm_off = [&](int c) { return rb ^ (32 * c); };
+  // Transpose read of rows 16k + r (r = 4(lane/32) + (lane%16)/4, +8 for
+  // hf = 1), columns 32dt + 16((lane/16)%2) + 4(lane%4) of a 256 B-row tile:
+  // 16((4dt + q) ^ swz(r)) = 64(dt ^ (r & 3)) + 16(q ^ ((r >> 2) & 3)).
   const int tr_r0 = 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_q = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-  const int tr_b = 8 * (lane & 1);
-  auto toff = [&](int hf, int dt) {
+  auto tr_base = [&](int hf) {
     const int r = tr_r0 + 8 * hf;
-    return r * S::ROWB + 16 * ((4 * dt + tr_q) ^ swz_chunk(r)) + tr_b;
+    return r * S::ROWB + 64 * (r & 3) + 16 * (tr_q ^ ((r >> 2) & 3)) + 8 * (lane & 1);
   };
+  const int tb0_base = tr_base(0), tb1_base = tr_base(1);
+  int tb0 = tb0_base, tb1 = tb1_base;
+  auto toff = [&](int hf, int dt) { return (hf ? tb1 : tb0) ^ (64 * dt); };
+  // dSᵀ row 32w + lr, piece 2g + lh: 8((2g + lh) ^ m) with m = (row >> 2) & 7
+  // = 16(g ^ (m >> 1)) + 8(lh ^ (m & 1)).
+  const int dsw_row = 32 * wave + lr;
+  const int dsw_m = (dsw_row >> 2) & 7;
+  const int dsw_base = dsw_row * S::DS_ROWB + 16 * (dsw_m >> 1) + 8 * (lh ^ (dsw_m & 1));
+  int dw = dsw_base;
+  auto dsw_off = [&](int g) { return dw ^ (16 * g); };
   // dSᵀ transpose reads: rows 16kc + r, piece 4((k/16)%2) + k%4.
   const int ds_r = 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int ds_p = 4 * ((lane >> 4) & 1) + (lane & 3);
@@ -118,30 +136,45 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
   const int nit = max(it1 - it0, 0);
   const int ntot = nit * G;
   const int wkv_last = min(kv0w + 31, Sk - 1);
+  const int64_t head_rows = (int64_t)b * H + hk * G;  // (b, first query head) row block
 
-  // Iteration t: query head hk*G + t / nit, query tile it0 + t % nit.
-  auto issue_q = [&](int t, char* qb, char* ob, float* st) {
-    const int h = hk * G + t / nit;
-    const int i0 = (it0 + t % nit) * S::BQ;
+  // Tile t covers query head hk*G + t / nit and query tile it0 + t % nit;
+  // (h_rel, it) is carried incrementally so the loop has no integer division.
+  auto issue_q = [&](int h_rel, int it, char* qb, char* ob, float* st) {
+    const int h = hk * G + h_rel;
+    const int i0 = it * S::BQ;
     const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] + h * a.q_stride[2];
     const uint16_t* og = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
                          h * a.do_stride[2];
-    const int r = 4 * wave + (lane >> 4);
-    const int c = (lane & 15) ^ swz_chunk(r);
-    const int i = min(i0 + r, Sq - 1);
-    load_lds16(qg + (int64_t)i * a.q_stride[1] + 8 * c, qb + wave * 1024);
-    load_lds16(og + (int64_t)i * a.do_stride[1] + 8 * c, ob + wave * 1024);
+    // 32 rows = 8 blocks of 1 KB per tile; each wave loads 8 / NW of them.
+    constexpr int BPW = 8 / S::NW;
+#pragma unroll
+    for (int ii = 0; ii < BPW; ++ii) {
+      const int blk = BPW * wave + ii;
+      const int r = 4 * blk + (lane >> 4);
+      const int c = (lane & 15) ^ swz_chunk(r);
+      const int i = min(i0 + r, Sq - 1);
+      load_lds16(qg + (int64_t)i * a.q_stride[1] + 8 * c, qb + blk * 1024);
+      load_lds16(og + (int64_t)i * a.do_stride[1] + 8 * c, ob + blk * 1024);
+    }
     if (wave == 0) {
-      const int64_t stat0 = ((int64_t)b * H + h) * Sq;
-      const int ii = min(i0 + (lane & 31), Sq - 1);
-      const float* src = (lane < 32) ? lse2 + stat0 + ii : rowdot + stat0 + ii;
+      // Lanes 0-31 fetch LSE*log2(e), lanes 32-63 rowdot ([B*H][2][Sq]).
+      const float* sbase = stats + 2 * (head_rows + h_rel) * Sq + i0;
+      const float* src = sbase + ((lane >> 5) * Sq + min(lane & 31, Sq - 1 - i0));
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)st, 4, 0, 0);
     }
   };
 
-  auto step = [&](int t, const char* qb, const char* ob, const float* st) {
-    const int h = hk * G + t / nit;
-    const int i0 = (it0 + t % nit) * S::BQ;
+  auto step = [&](int h_rel, int it, const char* qb, const char* ob, const float* st) {
+    // The per-chunk offsets are `base ^ constant`.  Re-deriving the bases as
+    // opaque values each iteration keeps the compiler from hoisting every
+    // XOR result out of the loop into a register of its own.
+    rb = rm_base;
+    tb0 = tb0_base;
+    tb1 = tb1_base;
+    dw = dsw_base;
+    asm volatile("" : "+v"(rb), "+v"(tb0), "+v"(tb1), "+v"(dw));
+    const int i0 = it * S::BQ;
     const bool active = (!CAUSAL || (i0 + S::BQ - 1 + off >= kv0w)) && kv0w < Sk;
     if (active) {
       f32x16 s, dp;
@@ -155,6 +188,9 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
         s = T::mma32(aq, bk, s);
         dp = T::mma32(ao, vB[c], dp);
       }
+      // Keep two chunks of operands in flight: loads of chunk c + 2 are
+      // issued between the products of chunk c (bounds register use).
+      sched_pipeline<D / 16, 3, 2, 2>();
       // s[i], dp[i]: query i0 + 8(i/4) + 4lh + (i%4), key my_kv.
       const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kv0w + 32 > Sk) ||
                              (i0 + S::BQ > Sq);
@@ -190,7 +226,7 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
       for (int g = 0; g < 4; ++g) {
         const int kq = g >> 1, w0 = 2 * (g & 1);
         const u32x2 v = {sB[kq][w0], sB[kq][w0 + 1]};
-        st8(dSt + ds_piece(32 * wave + lr, 2 * g + lh), v);
+        st8(dSt + dsw_off(g), v);
       }
       // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads)
 #pragma unroll
@@ -207,15 +243,16 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
           dv[dt] = T::mma32(ao, pB[kq], dv[dt]);
           dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
         }
+      sched_pipeline<2 * (D / 32), 4, 2, 2>();
     } else {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) st8(dSt + ds_piece(32 * wave + lr, 2 * g + lh), u32x2{0, 0});
+      for (int g = 0; g < 4; ++g) st8(dSt + dsw_off(g), u32x2{0, 0});
     }
     __syncthreads();  // dSᵀ complete
 
-    // dQ[i0 + q][32w + d] += sum over the 256 keys, waves 0..3 (one 32-wide d tile each).
+    // dQ[i0 + q][32w + d] += sum over the workgroup's keys (waves 0 .. DQW-1).
     const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
-    if (wave < 4 && any) {
+    if (wave < S::DQW && any) {
       const int dt = wave;
       f32x16 acc;
 #pragma unroll
@@ -234,37 +271,56 @@ __global__ __launch_bounds__(512, 2) void bwd_main_d128_kernel(fa_bwd_args a, fl
         const u32x4 bk = {k_lo[0], k_lo[1], k_hi[0], k_hi[1]};
         acc = T::mma32(as, bk, acc);
       }
+      sched_pipeline<S::BKV / 16, 4, 1, 3>();
       // acc[4g + r] = dQ[query i0 + 8g + 4lh + r][d 32dt + lr]; dqacc is
-      // [B, H, Sq, D], so row r of group g is an immediate offset r*D.
-      float* dqh = dqacc + (((int64_t)b * H + h) * Sq + i0 + 4 * lh) * D + 32 * dt + lr;
+      // [B, H, Sq, D].  The base is uniform; lanes add a 32-bit offset.
+      float* dqh = dqacc + ((head_rows + h_rel) * Sq + i0) * D + 32 * dt;
+      const int lo = 4 * lh * D + lr;
       if (i0 + S::BQ <= Sq) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float* pg = dqh + 8 * g * D;
+        for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) unsafeAtomicAdd(pg + r * D, acc[4 * g + r]);
-        }
+          for (int r = 0; r < 4; ++r) unsafeAtomicAdd(dqh + lo + (8 * g + r) * D, acc[4 * g + r]);
       } else {
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (i0 + 8 * g + 4 * lh + r < Sq) unsafeAtomicAdd(dqh + (8 * g + r) * D, acc[4 * g + r]);
+            if (i0 + 8 * g + 4 * lh + r < Sq) unsafeAtomicAdd(dqh + lo + (8 * g + r) * D, acc[4 * g + r]);
       }
     }
   };
 
-  if (ntot > 0) issue_q(0, Q0, O0, st0);
+  int ih = 0, ii = it0;  // tile to issue next
+  int ch = 0, ci = it0;  // tile to compute next
+  auto advance = [&](int& h_rel, int& it) {
+    if (++it == it1) {
+      it = it0;
+      ++h_rel;
+    }
+  };
+  if (ntot > 0) {
+    issue_q(ih, ii, Q0, O0, st0);
+    advance(ih, ii);
+  }
   for (int t = 0; t < ntot; t += 2) {
     wait_vmem();
     __syncthreads();  // tile t (and K on the first pass) resident; dSᵀ free
-    if (t + 1 < ntot) issue_q(t + 1, Q1, O1, st1);
-    step(t, Q0, O0, st0);
+    if (t + 1 < ntot) {
+      issue_q(ih, ii, Q1, O1, st1);
+      advance(ih, ii);
+    }
+    step(ch, ci, Q0, O0, st0);
+    advance(ch, ci);
     if (t + 1 >= ntot) break;
     wait_vmem();
     __syncthreads();
-    if (t + 2 < ntot) issue_q(t + 2, Q0, O0, st0);
-    step(t + 1, Q1, O1, st1);
+    if (t + 2 < ntot) {
+      issue_q(ih, ii, Q0, O0, st0);
+      advance(ih, ii);
+    }
+    step(ch, ci, Q1, O1, st1);
+    advance(ch, ci);
   }
   wait_vmem();
 

@@ -127,6 +127,21 @@ __device__ __forceinline__ void st8(void* p, u32x2 v) {
   *reinterpret_cast<u32x2*>(p) = v;
 }
 
+// Instruction-scheduling hint for a loop of N steps that each issue L LDS
+// reads followed by M matrix products: the reads of the first `ahead` steps
+// go first, then every step's products are followed by the reads of step
+// + ahead.  Applies to the code emitted before it in the same basic block.
+template <int N, int L, int M, int ahead>
+__device__ __forceinline__ void sched_pipeline() {
+  constexpr int kDsRead = 0x100, kMfma = 0x008;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, L * ahead, 0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, M, 0);
+    if (i + ahead < N) __builtin_amdgcn_sched_group_barrier(kDsRead, L, 0);
+  }
+}
+
 // XCD-aware workgroup order.  The hardware hands consecutive workgroup ids to
 // the 8 XCDs round-robin; remapping makes each XCD receive a contiguous range
 // of logical tiles, so tiles that share K/V rows share one L2.
