@@ -7,18 +7,22 @@
 //  * NW waves x 32 keys per workgroup (NW = 8: 256 keys), so the fp32
 //    atomics that reduce dQ across key tiles cover 256 keys each and every
 //    Q / dO tile fetched into LDS serves 256 keys.
-//  * The workgroup's K tile (128 x 256 B) is copied once HBM -> LDS with
+//  * The workgroup's K tile (256 x 256 B) is copied once HBM -> LDS with
 //    global_load_lds_dwordx4 and serves as the B operand of S (row reads)
 //    and of dQ (transpose reads).  V rows of each wave stay in registers.
 //  * Q and dO tiles (32 rows) are DMA'd the same way, double-buffered in
 //    distinct arrays (see attn_fwd_tile_d128 for why distinct arrays).
 //    Qᵀ / dOᵀ operands come from ds_read_b64_tr_b16; nothing is transposed
 //    in registers.
-//  * dSᵀ goes to LDS with 8-byte stores (its 8-byte pieces XOR-swizzled by
-//    row so both the stores and the transpose reads are conflict free) and
-//    is read back transposed as the A operand of dQ.  Each wave computes
-//    the 32 x 32 dQ block of one 32-wide d tile over all 128 keys and adds
-//    it to the fp32 accumulator with one atomic per element.
+//  * dSᵀ goes to LDS (double-buffered) with 8-byte stores (its 8-byte
+//    pieces XOR-swizzled by row so both the stores and the transpose reads
+//    are conflict free) and
+//    is read back transposed as the A operand of dQ.  Waves 0-3 each
+//    compute the 32 x 32 dQ block of one 32-wide d tile over all keys of
+//    the workgroup, one iteration later (after the single barrier of the
+//    next iteration), so the dQ products overlap the other waves' S / dP
+//    products, and add it to the fp32 accumulator with one atomic per
+//    element.
 //  * 256-byte K / Q / dO rows use the 16-byte-chunk swizzle of
 //    fa_fwd_d128.h.
 #pragma once
@@ -38,7 +42,7 @@ struct BwdShapeD128 {
   static constexpr int K_BYTES = BKV * ROWB;  // 64 KB
   static constexpr int QT_BYTES = BQ * ROWB;  // 8 KB
   static constexpr int DS_ROWB = BQ * 2;      // 64 B per dSᵀ row
-  static constexpr int DS_BYTES = BKV * DS_ROWB;
+  static constexpr int DS_BYTES = BKV * DS_ROWB;  // 16 KB, double-buffered
   static constexpr int DQW = D / 32;          // waves computing dQ (one d tile each)
   static_assert(NW >= DQW && (8 % NW) == 0, "tile loader / dQ split");
 };
@@ -52,7 +56,7 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
   __shared__ __attribute__((aligned(16))) char Q0[S::QT_BYTES], O0[S::QT_BYTES];
   __shared__ __attribute__((aligned(16))) char Q1[S::QT_BYTES], O1[S::QT_BYTES];
   __shared__ __attribute__((aligned(16))) float st0[2 * S::BQ], st1[2 * S::BQ];
-  __shared__ __attribute__((aligned(16))) char dSt[S::DS_BYTES];
+  __shared__ __attribute__((aligned(16))) char dS0[S::DS_BYTES], dS1[S::DS_BYTES];
 
   const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads, Hk = a.num_heads_k;
   const int G = H / Hk;
@@ -165,7 +169,9 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
     }
   };
 
-  auto step = [&](int h_rel, int it, const char* qb, const char* ob, const float* st) {
+  // S, dP, softmax, dSᵀ -> dsb, dV and dK for one query tile (no barrier).
+  auto step = [&](int h_rel, int it, const char* qb, const char* ob, const float* st,
+                  char* dsb) {
     // The per-chunk offsets are `base ^ constant`.  Re-deriving the bases as
     // opaque values each iteration keeps the compiler from hoisting every
     // XOR result out of the loop into a register of its own.
@@ -226,7 +232,7 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
       for (int g = 0; g < 4; ++g) {
         const int kq = g >> 1, w0 = 2 * (g & 1);
         const u32x2 v = {sB[kq][w0], sB[kq][w0 + 1]};
-        st8(dSt + dsw_off(g), v);
+        st8(dsb + dsw_off(g), v);
       }
       // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads)
 #pragma unroll
@@ -246,11 +252,14 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
       sched_pipeline<2 * (D / 32), 4, 2, 2>();
     } else {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) st8(dSt + dsw_off(g), u32x2{0, 0});
+      for (int g = 0; g < 4; ++g) st8(dsb + dsw_off(g), u32x2{0, 0});
     }
-    __syncthreads();  // dSᵀ complete
+  };
 
-    // dQ[i0 + q][32w + d] += sum over the workgroup's keys (waves 0 .. DQW-1).
+  // dQ[i0 + q][32w + d] += sum over the workgroup's keys of dS K, for the
+  // tile whose dSᵀ is complete in dsb (waves 0 .. DQW-1, one d tile each).
+  auto dq_step = [&](int h_rel, int it, const char* dsb) {
+    const int i0 = it * S::BQ;
     const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
     if (wave < S::DQW && any) {
       const int dt = wave;
@@ -260,9 +269,9 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
 #pragma unroll
       for (int kc = 0; kc < S::BKV / 16; ++kc) {
         const int par = 4 * (kc & 1);
-        const u32x2 s_lo = lds_read_tr(dSt + (16 * kc + ds_r) * S::DS_ROWB +
+        const u32x2 s_lo = lds_read_tr(dsb + (16 * kc + ds_r) * S::DS_ROWB +
                                        8 * (ds_p ^ ((ds_r >> 2) + par)));
-        const u32x2 s_hi = lds_read_tr(dSt + (16 * kc + ds_r + 8) * S::DS_ROWB +
+        const u32x2 s_hi = lds_read_tr(dsb + (16 * kc + ds_r + 8) * S::DS_ROWB +
                                        8 * (ds_p ^ (((ds_r + 8) >> 2) + par)));
         const int ro = kc * 16 * S::ROWB;
         const u32x2 k_lo = lds_read_tr(Ks + toff(0, dt) + ro);
@@ -299,28 +308,46 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
       ++h_rel;
     }
   };
+  // Iteration t: one barrier (Q/dO tile t landed, dSᵀ of tile t-1 complete,
+  // buffers of tile t-1 free), then the DMA of tile t+1, the dQ product of
+  // tile t-1 (waves 0..3, overlapping the other waves' products of tile t)
+  // and tile t's products.  dSᵀ alternates between dS0 and dS1.
+  int ph = 0, pi = 0;  // tile whose dQ is pending
   if (ntot > 0) {
     issue_q(ih, ii, Q0, O0, st0);
     advance(ih, ii);
   }
   for (int t = 0; t < ntot; t += 2) {
     wait_vmem();
-    __syncthreads();  // tile t (and K on the first pass) resident; dSᵀ free
+    __syncthreads();
     if (t + 1 < ntot) {
       issue_q(ih, ii, Q1, O1, st1);
       advance(ih, ii);
     }
-    step(ch, ci, Q0, O0, st0);
+    if (t > 0) dq_step(ph, pi, dS1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the two phases' registers apart
+    step(ch, ci, Q0, O0, st0, dS0);
+    ph = ch;
+    pi = ci;
     advance(ch, ci);
-    if (t + 1 >= ntot) break;
-    wait_vmem();
-    __syncthreads();
-    if (t + 2 < ntot) {
-      issue_q(ih, ii, Q0, O0, st0);
-      advance(ih, ii);
+    if (t + 1 < ntot) {
+      wait_vmem();
+      __syncthreads();
+      if (t + 2 < ntot) {
+        issue_q(ih, ii, Q0, O0, st0);
+        advance(ih, ii);
+      }
+      dq_step(ph, pi, dS0);
+      __builtin_amdgcn_sched_barrier(0);
+      step(ch, ci, Q1, O1, st1, dS1);
+      ph = ch;
+      pi = ci;
+      advance(ch, ci);
     }
-    step(ch, ci, Q1, O1, st1);
-    advance(ch, ci);
+  }
+  if (ntot > 0) {
+    __syncthreads();  // dSᵀ of the last tile complete
+    dq_step(ph, pi, ((ntot - 1) & 1) ? dS1 : dS0);
   }
   wait_vmem();
 
