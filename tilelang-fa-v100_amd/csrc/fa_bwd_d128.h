@@ -61,9 +61,10 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
   const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads, Hk = a.num_heads_k;
   const int G = H / Hk;
   const int kvtiles = (Sk + S::BKV - 1) / S::BKV;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int kt_idx = id % kvtiles;  // smallest key index first: most query rows
-  const int bh = id / kvtiles;
+  // Rank 0 = key tile 0, which sees the most query rows when causal.
+  const TileHead th = xcd_tile_order(blockIdx.x, kvtiles, a.batch * Hk);
+  const int kt_idx = th.rank;
+  const int bh = th.bh;
   const int hk = bh % Hk, b = bh / Hk;
   const int kv0 = kt_idx * S::BKV;
   const int off = Sk - Sq;  // key n visible to query i iff n <= i + off

@@ -142,6 +142,27 @@ __device__ __forceinline__ void sched_pipeline() {
   }
 }
 
+// Workgroup order for a grid of ntiles x nbh tiles (nbh = batch x heads).
+// The hardware hands workgroup ids to the 8 XCDs round-robin and each XCD
+// starts its ids in increasing order.  Each XCD is given a contiguous block
+// of heads (tiles of one head share K/V or Q/dO in that XCD's L2), and within
+// its heads it starts every head's rank-0 tile, then every rank-1 tile, and
+// so on; with rank 0 the most expensive causal tile, long tiles start first
+// and short ones fill the tail.  Falls back to rank-major over all heads when
+// nbh is not a multiple of 8.
+struct TileHead {
+  int rank, bh;
+};
+__device__ __forceinline__ TileHead xcd_tile_order(int wg, int ntiles, int nbh) {
+  constexpr int kXcds = 8;
+  if (nbh % kXcds == 0) {
+    const int per = nbh / kXcds;
+    const int local = wg / kXcds;
+    return {local / per, (wg % kXcds) * per + local % per};
+  }
+  return {wg / nbh, wg % nbh};
+}
+
 // XCD-aware workgroup order.  The hardware hands consecutive workgroup ids to
 // the 8 XCDs round-robin; remapping makes each XCD receive a contiguous range
 // of logical tiles, so tiles that share K/V rows share one L2.

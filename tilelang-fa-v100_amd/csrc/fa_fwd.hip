@@ -72,13 +72,12 @@ __global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PE
 void fwd_dense_kernel(fa_fwd_args a) {
   using C = FwdKernelCfg<D>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt_raw = id % qtiles;
-  const int bh = id / qtiles;
+  const TileHead th = xcd_tile_order(blockIdx.x, qtiles, a.batch * a.num_heads);
+  const int bh = th.bh;
   const int h = bh % a.num_heads;
   const int b = bh / a.num_heads;
   // Heaviest causal tiles (largest query index) first.
-  const int qt = CAUSAL ? qtiles - 1 - qt_raw : qt_raw;
+  const int qt = CAUSAL ? qtiles - 1 - th.rank : th.rank;
   const int hk = h / (a.num_heads / a.num_heads_k);
 
   DenseRows P;
