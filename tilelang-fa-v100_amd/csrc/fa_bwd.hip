@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
   const int kv0 = kt_idx * S::BKV;
   const int off = Sk - Sq;  // key n visible to query i iff n <= i + off
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
   const int kv0w = kv0 + 32 * wave;
   const int my_kv = kv0w + lr;
@@ -422,17 +422,17 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if constexpr (D == 128) {
-    using S2 = BwdShapeD128;
+    using S2 = BwdShapeD128<kBwdKB>;
     const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
     } else if (a.causal)
-      hipLaunchKernelGGL((bwd_main_d128_kernel<T, true>), grid, dim3(64 * S2::NW), 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_d128_kernel<T, true, kBwdKB>), grid, dim3(64 * S2::NW), 0, st,
+                         a, dqacc, stats);
     else
-      hipLaunchKernelGGL((bwd_main_d128_kernel<T, false>), grid, dim3(64 * S2::NW), 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_d128_kernel<T, false, kBwdKB>), grid, dim3(64 * S2::NW), 0,
+                         st, a, dqacc, stats);
   } else {
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);

@@ -4,25 +4,27 @@
 // tile) the 5 products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS and
 // dQ += dS K, with P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot).
 // Layout, for the gfx950 memory instructions:
-//  * NW waves x 32 keys per workgroup (NW = 8: 256 keys), so the fp32
-//    atomics that reduce dQ across key tiles cover 256 keys each and every
-//    Q / dO tile fetched into LDS serves 256 keys.
+//  * 256 keys per workgroup: NW = 8 / KB waves, each owning KB blocks of 32
+//    keys.  The fp32 atomics that reduce dQ across key tiles then cover 256
+//    keys each, and every Q / dO tile fetched into LDS serves 256 keys.
+//    With KB = 2 (4 waves, one per SIMD) a wave has 512 registers, holds
+//    dK / dV of 64 keys, and every Q / dO operand it reads from LDS feeds
+//    the products of both its key blocks.
 //  * The workgroup's K tile (256 x 256 B) is copied once HBM -> LDS with
 //    global_load_lds_dwordx4 and serves as the B operand of S (row reads)
 //    and of dQ (transpose reads).  V rows of each wave stay in registers.
-//  * Q and dO tiles (32 rows) are DMA'd the same way, double-buffered in
-//    distinct arrays (see attn_fwd_tile_d128 for why distinct arrays).
-//    Qᵀ / dOᵀ operands come from ds_read_b64_tr_b16; nothing is transposed
-//    in registers.
+//  * Q and dO tiles (32 rows) are DMA'd through buffer resources
+//    (buffer_load_dwordx4 ... lds), double-buffered in distinct arrays (see
+//    attn_fwd_tile_d128 for why distinct arrays).  Qᵀ / dOᵀ operands come
+//    from ds_read_b64_tr_b16; nothing is transposed in registers.
 //  * dSᵀ goes to LDS (double-buffered) with 8-byte stores (its 8-byte
 //    pieces XOR-swizzled by row so both the stores and the transpose reads
-//    are conflict free) and
-//    is read back transposed as the A operand of dQ.  Waves 0-3 each
-//    compute the 32 x 32 dQ block of one 32-wide d tile over all keys of
-//    the workgroup, one iteration later (after the single barrier of the
-//    next iteration), so the dQ products overlap the other waves' S / dP
-//    products, and add it to the fp32 accumulator with one atomic per
-//    element.
+//    are conflict free) and is read back transposed as the A operand of dQ.
+//    Four waves each compute the 32 x 32 dQ block of one 32-wide d tile over
+//    all keys of the workgroup, one iteration later (after the single
+//    barrier of the next iteration), so the dQ products overlap the S / dP
+//    products of the next tile, and add it to the fp32 accumulator with
+//    buffer atomics.
 //  * 256-byte K / Q / dO rows use the 16-byte-chunk swizzle of
 //    fa_fwd_d128.h.
 #pragma once
@@ -33,24 +35,30 @@
 
 namespace fa {
 
+template <int KB>
 struct BwdShapeD128 {
   static constexpr int D = 128;
-  static constexpr int NW = 8;        // waves per workgroup
-  static constexpr int BKV = 32 * NW; // keys per workgroup (32 per wave)
-  static constexpr int BQ = 32;       // query rows per iteration
+  static constexpr int NW = 8 / KB;         // waves per workgroup
+  static constexpr int BKV = 32 * KB * NW;  // 256 keys per workgroup
+  static constexpr int BQ = 32;             // query rows per iteration
   static constexpr int ROWB = 256;
   static constexpr int K_BYTES = BKV * ROWB;  // 64 KB
   static constexpr int QT_BYTES = BQ * ROWB;  // 8 KB
   static constexpr int DS_ROWB = BQ * 2;      // 64 B per dSᵀ row
   static constexpr int DS_BYTES = BKV * DS_ROWB;  // 16 KB, double-buffered
   static constexpr int DQW = D / 32;          // waves computing dQ (one d tile each)
-  static_assert(NW >= DQW && (8 % NW) == 0, "tile loader / dQ split");
+  static constexpr int WPE = NW / 4;          // waves per SIMD
+  static_assert(KB == 1 || KB == 2, "key blocks per wave");
+  static_assert(NW >= DQW, "dQ split");
 };
 
-template <class T, bool CAUSAL>
-__global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc,
-                                                               const float* stats) {
-  using S = BwdShapeD128;
+// Key blocks per wave used by the launcher.
+constexpr int kBwdKB = 1;
+
+template <class T, bool CAUSAL, int KB>
+__global__ __launch_bounds__(64 * BwdShapeD128<KB>::NW, BwdShapeD128<KB>::WPE)
+void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
+  using S = BwdShapeD128<KB>;
   constexpr int D = S::D;
   __shared__ __attribute__((aligned(16))) char Ks[S::K_BYTES];
   __shared__ __attribute__((aligned(16))) char Q0[S::QT_BYTES], O0[S::QT_BYTES];
@@ -69,42 +77,45 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
   const int kv0 = kt_idx * S::BKV;
   const int off = Sk - Sq;  // key n visible to query i iff n <= i + off
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
-  const int kv0w = kv0 + 32 * wave;
-  const int my_kv = kv0w + lr;
+  // Key block kb of this wave: keys kvb(kb) .. kvb(kb) + 31; lane key kvb + lr.
+  const int wrow = 32 * KB * wave;  // first key row of the wave within the tile
+  auto kvb = [&](int kb) { return kv0 + wrow + 32 * kb; };
   const float scale_log2 = a.softmax_scale * kLog2e;
 
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
 
-  // ---- K tile -> LDS (wave w: 1 KB blocks 8w .. 8w+7 = rows 32w .. 32w+31)
+  // ---- K tile -> LDS: 64 blocks of 1 KB (4 rows each); wave w loads
+  // blocks 8 KB w .. 8 KB w + 8 KB - 1 = its own key rows.
 #pragma unroll
-  for (int ii = 0; ii < 8; ++ii) {
-    const int blk = 8 * wave + ii;
+  for (int ii = 0; ii < 8 * KB; ++ii) {
+    const int blk = 8 * KB * wave + ii;
     const int r = 4 * blk + (lane >> 4);
     const int c = (lane & 15) ^ swz_chunk(r);
     const int n = min(kv0 + r, Sk - 1);
     load_lds16(kg + (int64_t)n * a.k_stride[1] + 8 * c, Ks + blk * 1024);
   }
   // ---- V rows of this wave (B operand of dP = dO Vᵀ)
-  u32x4 vB[D / 16];
-  {
-    const uint16_t* vp = vg + (int64_t)min(my_kv, Sk - 1) * a.v_stride[1];
+  u32x4 vB[KB][D / 16];
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) vB[c] = ld16(vp + 16 * c + 8 * lh);
+  for (int kb = 0; kb < KB; ++kb) {
+    const uint16_t* vp = vg + (int64_t)min(kvb(kb) + lr, Sk - 1) * a.v_stride[1];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) vB[kb][c] = ld16(vp + 16 * c + 8 * lh);
   }
 
   // ---- per-lane LDS offsets.  Chunk c of row r sits at chunk c ^ swz(r);
   // the chunk-index bits a product walks (c for row reads, the 64-byte d
   // tile for transpose reads) are free in the lane's base offset, so every
   // offset is that base XOR an instruction constant (one register per
-  // pattern instead of one per chunk).
+  // pattern instead of one per chunk).  Row offsets of 16-row multiples are
+  // instruction immediates.
   const int sw_lr = swz_chunk(lr);
   // Row read of chunk pair c (row lr, chunk 2c + lh):
   // 16((2c + lh) ^ sw) = 32(c ^ (sw >> 1)) + 16(lh ^ (sw & 1)).
-  const int rm_base = lr * S::ROWB + 16 * (lh ^ (sw_lr & 1)) + 32 * (sw_lr >> 1);
-  int rb = rm_base;  // opaque per-iteration copy, see `step`
+  int rb = lr * S::ROWB + 16 * (lh ^ (sw_lr & 1)) + 32 * (sw_lr >> 1);
   auto rm_off = [&](int c) { return rb ^ (32 * c); };
   // Transpose read of rows 16k + r (r = 4(lane/32) + (lane%16)/4, +8 for
   // hf = 1), columns 32dt + 16((lane/16)%2) + 4(lane%4) of a 256 B-row tile:
@@ -115,127 +126,165 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
     const int r = tr_r0 + 8 * hf;
     return r * S::ROWB + 64 * (r & 3) + 16 * (tr_q ^ ((r >> 2) & 3)) + 8 * (lane & 1);
   };
-  const int tb0_base = tr_base(0), tb1_base = tr_base(1);
-  int tb0 = tb0_base, tb1 = tb1_base;
+  int tb0 = tr_base(0), tb1 = tr_base(1);
   auto toff = [&](int hf, int dt) { return (hf ? tb1 : tb0) ^ (64 * dt); };
-  // dSᵀ row 32w + lr, piece 2g + lh: 8((2g + lh) ^ m) with m = (row >> 2) & 7
-  // = 16(g ^ (m >> 1)) + 8(lh ^ (m & 1)).
-  const int dsw_row = 32 * wave + lr;
-  const int dsw_m = (dsw_row >> 2) & 7;
-  const int dsw_base = dsw_row * S::DS_ROWB + 16 * (dsw_m >> 1) + 8 * (lh ^ (dsw_m & 1));
-  int dw = dsw_base;
-  auto dsw_off = [&](int g) { return dw ^ (16 * g); };
+  // dSᵀ row wrow + 32kb + lr, piece 2g + lh: 8((2g + lh) ^ m) with
+  // m = (row >> 2) & 7 = (lr >> 2) & 7 = 16(g ^ (m >> 1)) + 8(lh ^ (m & 1)).
+  const int dsw_m = (lr >> 2) & 7;
+  int dw = (wrow + lr) * S::DS_ROWB + 16 * (dsw_m >> 1) + 8 * (lh ^ (dsw_m & 1));
+  auto dsw_off = [&](int kb, int g) { return (dw ^ (16 * g)) + 32 * kb * S::DS_ROWB; };
   // dSᵀ transpose reads: rows 16kc + r, piece 4((k/16)%2) + k%4.
   const int ds_r = 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int ds_p = 4 * ((lane >> 4) & 1) + (lane & 3);
 
-  f32x16 dk[D / 32], dv[D / 32];
+  f32x16 dk[KB][D / 32], dv[KB][D / 32];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dk[kb][dt][i] = dv[kb][dt][i] = 0.f;
 
   const int q_begin = CAUSAL ? max(0, kv0 - off) : 0;
   const int it0 = q_begin / S::BQ;
   const int it1 = (Sq + S::BQ - 1) / S::BQ;
   const int nit = max(it1 - it0, 0);
   const int ntot = nit * G;
-  const int wkv_last = min(kv0w + 31, Sk - 1);
   const int64_t head_rows = (int64_t)b * H + hk * G;  // (b, first query head) row block
+
+  // Q / dO tile loader: 32 rows = 8 blocks of 1 KB; each wave loads 8 / NW
+  // of them.  Lane l of block blk holds row 4 blk + l/16, stored chunk l%16
+  // (logical chunk (l%16) ^ swz(row)); its byte offset from the tile's first
+  // row is fixed.
+  constexpr int BPW = 8 / S::NW;
+  uint32_t q_loff[BPW], o_loff[BPW];
+#pragma unroll
+  for (int ii = 0; ii < BPW; ++ii) {
+    const int r = 4 * (BPW * wave + ii) + (lane >> 4);
+    const uint32_t c = (lane & 15) ^ swz_chunk(r);
+    q_loff[ii] = 2u * (r * (uint32_t)a.q_stride[1] + 8 * c);
+    o_loff[ii] = 2u * (r * (uint32_t)a.do_stride[1] + 8 * c);
+  }
 
   // Tile t covers query head hk*G + t / nit and query tile it0 + t % nit;
   // (h_rel, it) is carried incrementally so the loop has no integer division.
   auto issue_q = [&](int h_rel, int it, char* qb, char* ob, float* st) {
     const int h = hk * G + h_rel;
     const int i0 = it * S::BQ;
-    const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] + h * a.q_stride[2];
-    const uint16_t* og = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
-                         h * a.do_stride[2];
-    // 32 rows = 8 blocks of 1 KB per tile; each wave loads 8 / NW of them.
-    constexpr int BPW = 8 / S::NW;
+    // Buffer resources over the tile's valid rows: rows at or past Sq read
+    // as zero (their products are masked), so no row clamping is needed.
+    const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] +
+                           h * a.q_stride[2] + (int64_t)i0 * a.q_stride[1];
+    const uint16_t* orow = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
+                           h * a.do_stride[2] + (int64_t)i0 * a.do_stride[1];
+    const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
+    const rsrc_t rq = make_rsrc(qrow, nrows * (uint32_t)a.q_stride[1] * 2u);
+    const rsrc_t ro = make_rsrc(orow, nrows * (uint32_t)a.do_stride[1] * 2u);
 #pragma unroll
     for (int ii = 0; ii < BPW; ++ii) {
       const int blk = BPW * wave + ii;
-      const int r = 4 * blk + (lane >> 4);
-      const int c = (lane & 15) ^ swz_chunk(r);
-      const int i = min(i0 + r, Sq - 1);
-      load_lds16(qg + (int64_t)i * a.q_stride[1] + 8 * c, qb + blk * 1024);
-      load_lds16(og + (int64_t)i * a.do_stride[1] + 8 * c, ob + blk * 1024);
+      buffer_lds16(rq, q_loff[ii], qb + blk * 1024);
+      buffer_lds16(ro, o_loff[ii], ob + blk * 1024);
     }
     if (wave == 0) {
       // Lanes 0-31 fetch LSE*log2(e), lanes 32-63 rowdot ([B*H][2][Sq]).
       const float* sbase = stats + 2 * (head_rows + h_rel) * Sq + i0;
-      const float* src = sbase + ((lane >> 5) * Sq + min(lane & 31, Sq - 1 - i0));
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)st, 4, 0, 0);
+      const unsigned lo = (lane >> 5) * Sq + min(lane & 31, Sq - 1 - i0);
+      __builtin_amdgcn_global_load_lds(sbase + lo, (__attribute__((address_space(3))) void*)st,
+                                       4, 0, 0);
     }
   };
 
   // S, dP, softmax, dSᵀ -> dsb, dV and dK for one query tile (no barrier).
   auto step = [&](int h_rel, int it, const char* qb, const char* ob, const float* st,
                   char* dsb) {
-    // The per-chunk offsets are `base ^ constant`.  Re-deriving the bases as
-    // opaque values each iteration keeps the compiler from hoisting every
-    // XOR result out of the loop into a register of its own.
-    rb = rm_base;
-    tb0 = tb0_base;
-    tb1 = tb1_base;
-    dw = dsw_base;
+    // The per-chunk offsets are `base ^ constant`.  Marking the bases as
+    // (opaquely) rewritten each iteration keeps the compiler from hoisting
+    // every XOR result out of the loop into a register of its own.
     asm volatile("" : "+v"(rb), "+v"(tb0), "+v"(tb1), "+v"(dw));
     const int i0 = it * S::BQ;
-    const bool active = (!CAUSAL || (i0 + S::BQ - 1 + off >= kv0w)) && kv0w < Sk;
+    // Key block 0 has the smallest keys: if it sees none of the tile's
+    // queries (or lies past Sk), no block of the wave does.
+    const bool active = (!CAUSAL || (i0 + S::BQ - 1 + off >= kvb(0))) && kvb(0) < Sk;
     if (active) {
-      f32x16 s, dp;
+      f32x16 s[KB], dp[KB];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[kb][i] = dp[kb][i] = 0.f;
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
         const u32x4 aq = ld16(qb + rm_off(c));
-        const u32x4 bk = ld16(Ks + 32 * wave * S::ROWB + rm_off(c));
         const u32x4 ao = ld16(ob + rm_off(c));
-        s = T::mma32(aq, bk, s);
-        dp = T::mma32(ao, vB[c], dp);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const u32x4 bk = ld16(Ks + (wrow + 32 * kb) * S::ROWB + rm_off(c));
+          s[kb] = T::mma32(aq, bk, s[kb]);
+          dp[kb] = T::mma32(ao, vB[kb][c], dp[kb]);
+        }
       }
       // Keep two chunks of operands in flight: loads of chunk c + 2 are
       // issued between the products of chunk c (bounds register use).
-      sched_pipeline<D / 16, 3, 2, 2>();
-      // s[i], dp[i]: query i0 + 8(i/4) + 4lh + (i%4), key my_kv.
-      const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kv0w + 32 > Sk) ||
-                             (i0 + S::BQ > Sq);
+      sched_pipeline<D / 16, 2 + KB, 2 * KB, 2>();
+
+      u32x4 pB[KB][2], sB[KB][2];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int qb4 = 8 * g + 4 * lh;
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + qb4);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + S::BQ + qb4);
+      for (int kb = 0; kb < KB; ++kb) {
+        const int kvw = kvb(kb);
+        const int my_kv = kvw + lr;
+        const int wkv_last = min(kvw + 31, Sk - 1);
+        const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kvw + 32 > Sk) ||
+                               (i0 + S::BQ > Sq);
+        // P = exp2(S·scale·log2e − lse2), dS = P (dP − rowdot).  Element
+        // (g, r) is query i0 + 8g + 4lh + r; on masked tiles it sees key
+        // my_kv iff c = 8g + r lies in [t_lo, t_hi); masked elements get
+        // P = 0.  The masked and unmasked forms are separate code paths so
+        // that the uniform branch between them stays a branch.
+        auto softmax = [&](auto masked) {
+          constexpr bool kMasked = decltype(masked)::value;
+          const int rel = i0 + 4 * lh;
+          const int t_lo = CAUSAL ? my_kv - off - rel : -0x40000000;
+          const int t_hi = (my_kv < Sk) ? Sq - rel : -0x40000000;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 4 * g + r;
-          float p = fast_exp2(fmaf(s[i], scale_log2, -l4[r]));
-          if (need_mask) {
-            const int qi = i0 + qb4 + r;
-            const bool vis = (my_kv < Sk) && (qi < Sq) && (!CAUSAL || my_kv <= qi + off);
-            p = vis ? p : 0.f;
+          for (int g = 0; g < 4; ++g) {
+            const int qb4 = 8 * g + 4 * lh;
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + qb4);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + S::BQ + qb4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int i = 4 * g + r;
+              float p = fast_exp2(fmaf(s[kb][i], scale_log2, -l4[r]));
+              if constexpr (kMasked) {
+                const int c = 8 * g + r;
+                p = (c >= t_lo && c < t_hi) ? p : 0.f;
+              }
+              s[kb][i] = p;
+              dp[kb][i] = p * (dp[kb][i] - d4[r]);
+            }
           }
-          s[i] = p;
-          dp[i] = p * (dp[i] - d4[r]);
+        };
+        if (need_mask)
+          softmax(BoolC<true>{});
+        else
+          softmax(BoolC<false>{});
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int e = 8 * kq + 2 * w;
+            pB[kb][kq][w] = T::pack(s[kb][e], s[kb][e + 1]);
+            sB[kb][kq][w] = T::pack(dp[kb][e], dp[kb][e + 1]);
+          }
+        // dSᵀ row wrow + 32kb + lr; queries 8g + 4lh .. +3 = piece 2g + lh.
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int kq = g >> 1, w0 = 2 * (g & 1);
+          const u32x2 v = {sB[kb][kq][w0], sB[kb][kq][w0 + 1]};
+          st8(dsb + dsw_off(kb, g), v);
         }
       }
-      u32x4 pB[2], sB[2];
-#pragma unroll
-      for (int kq = 0; kq < 2; ++kq)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int e = 8 * kq + 2 * w;
-          pB[kq][w] = T::pack(s[e], s[e + 1]);
-          sB[kq][w] = T::pack(dp[e], dp[e + 1]);
-        }
-      // dSᵀ row my_kv - kv0 = 32w + lr; queries 8g + 4lh .. +3 = piece 2g + lh.
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int kq = g >> 1, w0 = 2 * (g & 1);
-        const u32x2 v = {sB[kq][w0], sB[kq][w0 + 1]};
-        st8(dsb + dsw_off(g), v);
-      }
-      // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads)
+      // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads, shared
+      // by the wave's key blocks)
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq)
 #pragma unroll
@@ -247,13 +296,18 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
           const u32x2 q_hi = lds_read_tr(qb + toff(1, dt) + ro);
           const u32x4 ao = {o_lo[0], o_lo[1], o_hi[0], o_hi[1]};
           const u32x4 aq = {q_lo[0], q_lo[1], q_hi[0], q_hi[1]};
-          dv[dt] = T::mma32(ao, pB[kq], dv[dt]);
-          dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            dv[kb][dt] = T::mma32(ao, pB[kb][kq], dv[kb][dt]);
+            dk[kb][dt] = T::mma32(aq, sB[kb][kq], dk[kb][dt]);
+          }
         }
-      sched_pipeline<2 * (D / 32), 4, 2, 2>();
+      sched_pipeline<2 * (D / 32), 4, 2 * KB, 2>();
     } else {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) st8(dsb + dsw_off(g), u32x2{0, 0});
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) st8(dsb + dsw_off(kb, g), u32x2{0, 0});
     }
   };
 
@@ -283,21 +337,17 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
       }
       sched_pipeline<S::BKV / 16, 4, 1, 3>();
       // acc[4g + r] = dQ[query i0 + 8g + 4lh + r][d 32dt + lr]; dqacc is
-      // [B, H, Sq, D].  The base is uniform; lanes add a 32-bit offset.
-      float* dqh = dqacc + ((head_rows + h_rel) * Sq + i0) * D + 32 * dt;
-      const int lo = 4 * lh * D + lr;
-      if (i0 + S::BQ <= Sq) {
+      // [B, H, Sq, D].  The resource ends after column 31 of the tile's last
+      // valid row, so atomics for rows at or past Sq are dropped.
+      const float* dqh = dqacc + ((head_rows + h_rel) * Sq + i0) * D + 32 * dt;
+      const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
+      const rsrc_t rd = make_rsrc(dqh, ((nrows - 1) * D + 32) * 4u);
+      const uint32_t lo = 4u * (4 * lh * D + lr);
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) unsafeAtomicAdd(dqh + lo + (8 * g + r) * D, acc[4 * g + r]);
-      } else {
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (i0 + 8 * g + 4 * lh + r < Sq) unsafeAtomicAdd(dqh + lo + (8 * g + r) * D, acc[4 * g + r]);
-      }
+        for (int r = 0; r < 4; ++r)
+          buffer_atomic_add(rd, lo, 4u * (8 * g + r) * D, acc[4 * g + r]);
     }
   };
 
@@ -311,8 +361,8 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
   };
   // Iteration t: one barrier (Q/dO tile t landed, dSᵀ of tile t-1 complete,
   // buffers of tile t-1 free), then the DMA of tile t+1, the dQ product of
-  // tile t-1 (waves 0..3, overlapping the other waves' products of tile t)
-  // and tile t's products.  dSᵀ alternates between dS0 and dS1.
+  // tile t-1 (overlapping other waves' products of tile t) and tile t's
+  // products.  dSᵀ alternates between dS0 and dS1.
   int ph = 0, pi = 0;  // tile whose dQ is pending
   if (ntot > 0) {
     issue_q(ih, ii, Q0, O0, st0);
@@ -352,22 +402,25 @@ __global__ __launch_bounds__(64 * BwdShapeD128::NW, 2) void bwd_main_d128_kernel
   }
   wait_vmem();
 
-  if (my_kv < Sk) {
+  const float sc = a.softmax_scale;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int my_kv = kvb(kb) + lr;
+    if (my_kv >= Sk) continue;
     uint16_t* dkp = static_cast<uint16_t*>(a.dk) + b * a.dk_stride[0] +
                     (int64_t)my_kv * a.dk_stride[1] + hk * a.dk_stride[2];
     uint16_t* dvp = static_cast<uint16_t*>(a.dv) + b * a.dv_stride[0] +
                     (int64_t)my_kv * a.dv_stride[1] + hk * a.dv_stride[2];
-    const float sc = a.softmax_scale;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * dt + 8 * g + 4 * lh;
         u32x2 wk, wv;
-        wk[0] = T::pack(dk[dt][4 * g] * sc, dk[dt][4 * g + 1] * sc);
-        wk[1] = T::pack(dk[dt][4 * g + 2] * sc, dk[dt][4 * g + 3] * sc);
-        wv[0] = T::pack(dv[dt][4 * g], dv[dt][4 * g + 1]);
-        wv[1] = T::pack(dv[dt][4 * g + 2], dv[dt][4 * g + 3]);
+        wk[0] = T::pack(dk[kb][dt][4 * g] * sc, dk[kb][dt][4 * g + 1] * sc);
+        wk[1] = T::pack(dk[kb][dt][4 * g + 2] * sc, dk[kb][dt][4 * g + 3] * sc);
+        wv[0] = T::pack(dv[kb][dt][4 * g], dv[kb][dt][4 * g + 1]);
+        wv[1] = T::pack(dv[kb][dt][4 * g + 2], dv[kb][dt][4 * g + 3]);
         st8(dkp + d, wk);
         st8(dvp + d, wv);
       }

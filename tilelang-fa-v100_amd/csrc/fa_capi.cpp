@@ -50,6 +50,10 @@ bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
 constexpr int64_t kIntMax = 0x7fffffff;
 
+// Kernels address up to 32 rows past a uniform row base with unsigned 32-bit
+// offsets, so per-row (sequence) strides must stay below 2^26 elements.
+constexpr int64_t kMaxRowStride = int64_t(1) << 26;
+
 }  // namespace
 
 extern "C" {
@@ -123,9 +127,12 @@ static int check_bwd(const fa_bwd_args* a) {
     if (!aligned16(p)) return fail(FA_E_UNSUPPORTED, "fa_bwd: tensors must be 16-byte aligned");
   const int64_t* strides[] = {a->q_stride,  a->k_stride,  a->v_stride,  a->o_stride,
                               a->do_stride, a->dq_stride, a->dk_stride, a->dv_stride};
-  for (const int64_t* s : strides)
+  for (const int64_t* s : strides) {
     if (!strides_ok(s, 3))
       return fail(FA_E_UNSUPPORTED, "fa_bwd: strides must be non-negative multiples of 8");
+    if (s[1] >= kMaxRowStride)
+      return fail(FA_E_UNSUPPORTED, "fa_bwd: sequence strides must be below 2^26 elements");
+  }
   const int64_t tiles = ((int64_t)a->seqlen_k + 127) / 128 * a->num_heads_k * a->batch;
   const int64_t rows = (int64_t)a->batch * a->seqlen_q * a->num_heads;
   if (tiles > kIntMax || rows / 16 > kIntMax)

@@ -35,6 +35,12 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
+// Compile-time boolean tag (selects a code path through a generic lambda).
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+
 // Element-type traits.  `Half` is IEEE binary16, `BFloat16` is bfloat16.
 struct Half {
   static constexpr int kId = 0;
@@ -109,6 +115,13 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar)
+// value: branches on it then compile to scalar branches instead of EXEC
+// masking with both paths issued.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
 // Exchange with the lane 32 positions away (lane ^ 32).
 __device__ __forceinline__ float swap_halves(float x) {
   return __shfl_xor(x, 32);
@@ -140,6 +153,32 @@ __device__ __forceinline__ void sched_pipeline() {
     __builtin_amdgcn_sched_group_barrier(kMfma, M, 0);
     if (i + ahead < N) __builtin_amdgcn_sched_group_barrier(kDsRead, L, 0);
   }
+}
+
+// Buffer resources (gfx9 format): a 128-bit descriptor in scalar registers
+// plus a 32-bit per-lane byte offset.  Accesses at offsets >= `bytes` are
+// dropped (stores, atomics) or return zero (loads), which the kernels use to
+// cut ragged tiles without branches.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcFlags);
+}
+// 16 bytes per lane from base + voff into LDS (lane l writes lds_block + 16l).
+__device__ __forceinline__ void buffer_lds16(rsrc_t r, uint32_t voff, char* lds_block) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds_block, 16, voff, 0, 0, 0);
+}
+// 4 bytes per lane from base + voff into LDS (lane l writes lds_block + 4l).
+__device__ __forceinline__ void buffer_lds4(rsrc_t r, uint32_t voff, void* lds_block) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds_block, 4, voff, 0, 0, 0);
+}
+// Atomic fp32 add at base + voff + soff (no return value).
+__device__ __forceinline__ void buffer_atomic_add(rsrc_t r, uint32_t voff, uint32_t soff,
+                                                  float v) {
+  __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, voff, soff, 0);
 }
 
 // Workgroup order for a grid of ntiles x nbh tiles (nbh = batch x heads).

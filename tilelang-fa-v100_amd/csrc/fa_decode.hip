@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(fa_decode_args a,
   const int n_end = min(n_begin + CH, seq_len);
   const int n_last = n_end - 1;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int h0 = hk * G + hg * GB;  // first query head of this group
   const uint16_t* kc = static_cast<const uint16_t*>(a.k_cache) + (int64_t)hk * a.k_stride[2];
   const uint16_t* vc = static_cast<const uint16_t*>(a.v_cache) + (int64_t)hk * a.v_stride[2];

@@ -64,7 +64,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   const float scale_log2 = scale * kLog2e;
   constexpr float kLazy = 8.f;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
 
   const int nrows = P.nrows;
