@@ -144,15 +144,17 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     if (!(wave_active && n0 < w_hi_max && n0 + BN > w_lo_min)) return;
     f32x16 s[BN / 32];
 #pragma unroll
-    for (int kt = 0; kt < BN / 32; ++kt) {
-      u32x4 a[D / 16];
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) a[c] = ld16(kb + koff[c] + kt * 32 * S::ROWB);
+    for (int kt = 0; kt < BN / 32; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
+    // The key blocks' accumulation chains alternate (consecutive products are
+    // independent) and K reads run two chunks ahead of the products.
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) s[kt] = T::mma32(a[c], qf[c], s[kt]);
-    }
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int kt = 0; kt < BN / 32; ++kt)
+        s[kt] = T::mma32(ld16(kb + koff[c] + kt * 32 * S::ROWB), qf[c], s[kt]);
+    sched_pipeline<D / 16, BN / 32, BN / 32, 2>();
     const bool need_mask = (n0 < w_lo_max) || (n0 + BN > w_hi_min);
     if (need_mask) {
 #pragma unroll
