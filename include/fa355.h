@@ -215,6 +215,41 @@ int fa_paged_decode(const fa_decode_args* args, void* workspace,
                     size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* KV-cache write (vLLM reshape_and_cache).                                 */
+/*   key, value   [num_tokens, num_kv_heads, head_dim] (strides {token, head}) */
+/*   k/v_cache    [num_pages, page_size, num_kv_heads, head_dim]           */
+/*                (strides {page, slot, head}), the layout fa_paged_prefill */
+/*                and fa_paged_decode read                                  */
+/*   slot_mapping int64 [num_tokens]: token t goes to page slot_mapping[t] / */
+/*                page_size, slot slot_mapping[t] % page_size; a negative   */
+/*                entry (padding) or one >= num_pages * page_size is skipped */
+/* Several tokens mapped to one slot leave one of them there (unspecified   */
+/* which).                                                                  */
+/* ------------------------------------------------------------------------ */
+typedef struct fa_cache_write_args {
+  const void* key;
+  const void* value;
+  void* k_cache;
+  void* v_cache;
+  const int64_t* slot_mapping;
+  int64_t key_stride[2];
+  int64_t value_stride[2];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int32_t num_tokens;
+  int32_t num_kv_heads;
+  int32_t head_dim;    /* multiple of 8, at most 1024 */
+  int32_t page_size;   /* > 0 */
+  int32_t num_pages;
+  int32_t dtype;       /* fa_dtype of key, value and both caches */
+} fa_cache_write_args;
+
+/* No counterpart in the reference, which only reads this layout
+ * (_kernels_paged.py:198-199); it is the producer of the paged cache format
+ * (vLLM's reshape_and_cache).  No workspace. */
+int fa_reshape_and_cache(const fa_cache_write_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 int fa_abi_version(void);
 const char* fa_strerror(int status);
 /* Message of the most recent failing call on this thread ("" if none). */

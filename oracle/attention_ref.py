@@ -120,6 +120,26 @@ def dense_attention_backward(q, k, v, dout, scale=None, causal=False, dtype=torc
     return dq, dk, dv
 
 
+# --------------------------------------------------------------------- cache write
+
+def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
+    """In-place copy of key/value [T, Hkv, D] rows into [P, page, Hkv, D] caches.
+
+    The layout paged_rows reads (_kernels_paged.py:198-199, 265-272): token t
+    lands on page slot // page, slot slot % page.  Negative slots (padding)
+    and slots at or beyond P * page are skipped.  Written as a per-token loop
+    (the definition itself), not as the vectorised scatter the tests compare
+    with.
+    """
+    P, page = k_cache.shape[0], k_cache.shape[1]
+    for t in range(key.shape[0]):
+        s = int(slot_mapping[t])
+        if s < 0 or s >= P * page:
+            continue
+        k_cache[s // page, s % page] = key[t]
+        v_cache[s // page, s % page] = value[t]
+
+
 # --------------------------------------------------------------------- paged
 
 def paged_rows(cache, block_table_row, n):

@@ -43,7 +43,8 @@ def test_abi_version_and_strerror():
 
 
 STRUCTS = {"fa_fwd_args": _lib.FwdArgs, "fa_bwd_args": _lib.BwdArgs,
-           "fa_paged_args": _lib.PagedArgs, "fa_decode_args": _lib.DecodeArgs}
+           "fa_paged_args": _lib.PagedArgs, "fa_decode_args": _lib.DecodeArgs,
+           "fa_cache_write_args": _lib.CacheWriteArgs}
 
 
 def test_ctypes_structs_match_c_layout(tmp_path):
@@ -266,3 +267,46 @@ def test_public_api_matches_reference_signatures():
                                     "block_size", "num_kv_heads", "softmax_scale"]
     assert fa.__all__ == ["tilelang_flash_attn_func", "tilelang_flash_attn_gpu",
                           "tilelang_paged_forward", "tilelang_decode_forward"]
+    # The cache writer (no reference counterpart) follows vLLM's argument order.
+    sig = inspect.signature(fa.reshape_and_cache)
+    assert list(sig.parameters) == ["key", "value", "key_cache", "value_cache", "slot_mapping"]
+
+
+def test_reshape_and_cache_rejects_bad_arguments_before_launch():
+    k = torch.zeros(4, 2, 64, dtype=torch.float16)
+    kc = torch.zeros(3, 16, 2, 64, dtype=torch.float16)
+    slots = torch.arange(4)
+    with pytest.raises(TypeError):
+        fa.reshape_and_cache(k.float(), k, kc, kc, slots)
+    with pytest.raises(TypeError):
+        fa.reshape_and_cache(k, k, kc, kc, slots.float())
+    with pytest.raises(ValueError):
+        fa.reshape_and_cache(k, k[:, :1], kc, kc, slots)
+    with pytest.raises(ValueError):
+        fa.reshape_and_cache(k, k, kc[:, :, :1], kc[:, :, :1], slots)
+    with pytest.raises(ValueError):
+        fa.reshape_and_cache(k, k, kc, kc, slots[:3])
+    with pytest.raises(ValueError):  # CPU tensors: a GPU is required
+        fa.reshape_and_cache(k, k, kc, kc, slots)
+
+
+def test_cache_write_abi_rejects_bad_arguments():
+    lib = _lib.load()
+    a = _lib.CacheWriteArgs()
+    a.key = a.value = a.k_cache = a.v_cache = 0x1000
+    a.slot_mapping = 0x2000
+    a.key_stride[:] = (256, 128)
+    a.value_stride[:] = (256, 128)
+    a.k_stride[:] = (16 * 256, 256, 128)
+    a.v_stride[:] = (16 * 256, 256, 128)
+    a.num_tokens, a.num_kv_heads, a.head_dim, a.page_size, a.num_pages, a.dtype = 4, 2, 128, 16, 3, 0
+    bad = [("head_dim", 100), ("dtype", 7), ("page_size", 0), ("num_kv_heads", 0)]
+    for field, val in bad:
+        old = getattr(a, field)
+        setattr(a, field, val)
+        assert lib.fa_reshape_and_cache(ctypes.byref(a), None) != 0, field
+        setattr(a, field, old)
+    a.key = 0x1008  # misaligned
+    assert lib.fa_reshape_and_cache(ctypes.byref(a), None) == _lib.FA_E_UNSUPPORTED
+    a.key = 0
+    assert lib.fa_reshape_and_cache(ctypes.byref(a), None) == _lib.FA_E_INVALID

@@ -275,3 +275,60 @@ def test_planted_dropped_scale_in_dk_is_caught(gold, monkeypatch):
     monkeypatch.setattr(ref, "dense_attention_backward", no_scale_dk)
     with pytest.raises(AssertionError):
         test_backward_matches_finite_differences(gold)
+
+
+# ------------------------------------------------------------------ cache write (bit-exact)
+
+def _scatter_ref(key, value, kc, vc, slots):
+    """Vectorised restatement: flat [P*page] row view indexed by valid slots."""
+    P, page = kc.shape[:2]
+    keep = (slots >= 0) & (slots < P * page)
+    kf, vf = kc.reshape(P * page, *kc.shape[2:]), vc.reshape(P * page, *vc.shape[2:])
+    kf[slots[keep]] = key[keep]
+    vf[slots[keep]] = value[keep]
+
+
+def test_reshape_and_cache_matches_flat_scatter():
+    g = torch.Generator().manual_seed(9)
+    for page in (1, 4, 16):
+        P, T, Hkv, D = 7, 11, 3, 8
+        key, value = torch.randn(T, Hkv, D, generator=g), torch.randn(T, Hkv, D, generator=g)
+        slots = torch.randperm(P * page + 4, generator=g)[:T] - 2  # some < 0, some >= P*page
+        a = [torch.full((P, page, Hkv, D), -7.0) for _ in range(2)]
+        b = [x.clone() for x in a]
+        ref.reshape_and_cache(key, value, a[0], a[1], slots)
+        _scatter_ref(key, value, b[0], b[1], slots)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        written = ((slots >= 0) & (slots < P * page)).sum().item()
+        assert (a[0] != -7.0).all(-1).all(-1).sum().item() == written
+
+
+def test_reshape_and_cache_round_trips_through_paged_rows():
+    """Writer and reader agree: slots from a block table, read back in order."""
+    g = torch.Generator().manual_seed(10)
+    for page in (1, 16):
+        P, Hkv, D = 9, 2, 8
+        n = min(37, P * page)
+        key, value = torch.randn(n, Hkv, D, generator=g), torch.randn(n, Hkv, D, generator=g)
+        bt = torch.randperm(P, generator=g).to(torch.int32)
+        pos = torch.arange(n)
+        slots = bt[pos // page].long() * page + pos % page
+        kc = torch.zeros(P, page, Hkv, D)
+        vc = torch.zeros(P, page, Hkv, D)
+        ref.reshape_and_cache(key, value, kc, vc, slots)
+        assert torch.equal(ref.paged_rows(kc, bt, n), key)
+        assert torch.equal(ref.paged_rows(vc, bt, n), value)
+
+
+def test_planted_transposed_page_slot_is_caught(monkeypatch):
+    """A writer that swaps page and slot fails the round trip above."""
+    def bad(key, value, k_cache, v_cache, slot_mapping):
+        P, page = k_cache.shape[0], k_cache.shape[1]
+        for t in range(key.shape[0]):
+            s = int(slot_mapping[t])
+            if 0 <= s < P * page:
+                k_cache[s % P, s // P] = key[t]
+                v_cache[s % P, s // P] = value[t]
+    monkeypatch.setattr(ref, "reshape_and_cache", bad)
+    with pytest.raises(AssertionError):
+        test_reshape_and_cache_round_trips_through_paged_rows()

@@ -259,4 +259,37 @@ int fa_paged_decode(const fa_decode_args* a, void* ws, size_t ws_bytes, void* st
                     "fa_paged_decode launch");
 }
 
+// ------------------------------------------------------------------ cache write
+
+static int check_cache_write(const fa_cache_write_args* a) {
+  if (!a) return fail(FA_E_INVALID, "fa_reshape_and_cache: null args");
+  if (!a->key || !a->value || !a->k_cache || !a->v_cache || !a->slot_mapping)
+    return fail(FA_E_INVALID, "fa_reshape_and_cache: null pointer");
+  if (a->dtype != FA_DTYPE_F16 && a->dtype != FA_DTYPE_BF16)
+    return fail(FA_E_UNSUPPORTED, "fa_reshape_and_cache: dtype %d not supported", a->dtype);
+  if (a->head_dim <= 0 || (a->head_dim & 7) != 0 || a->head_dim > 1024)
+    return fail(FA_E_UNSUPPORTED, "fa_reshape_and_cache: head_dim %d not a multiple of 8 in "
+                "[8, 1024]", a->head_dim);
+  if (a->num_tokens < 0 || a->num_kv_heads <= 0 || a->num_pages < 0 || a->page_size <= 0)
+    return fail(FA_E_INVALID, "fa_reshape_and_cache: bad size");
+  if (!aligned16(a->key) || !aligned16(a->value) || !aligned16(a->k_cache) ||
+      !aligned16(a->v_cache))
+    return fail(FA_E_UNSUPPORTED, "fa_reshape_and_cache: tensors must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(a->slot_mapping) & 7u) != 0)
+    return fail(FA_E_INVALID, "fa_reshape_and_cache: slot_mapping must be 8-byte aligned");
+  if (!strides_ok(a->key_stride, 2) || !strides_ok(a->value_stride, 2) ||
+      !strides_ok(a->k_stride, 3) || !strides_ok(a->v_stride, 3))
+    return fail(FA_E_UNSUPPORTED,
+                "fa_reshape_and_cache: strides must be non-negative multiples of 8");
+  return ok();
+}
+
+int fa_reshape_and_cache(const fa_cache_write_args* a, void* stream) {
+  const int st = check_cache_write(a);
+  if (st != FA_OK) return st;
+  if (a->num_tokens == 0 || a->num_pages == 0) return ok();
+  return hip_status(fa::launch_cache_write(*a, static_cast<hipStream_t>(stream)),
+                    "fa_reshape_and_cache launch");
+}
+
 }  // extern "C"

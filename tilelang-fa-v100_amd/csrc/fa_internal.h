@@ -21,4 +21,6 @@ int decode_num_splits(const fa_decode_args& a);
 size_t decode_workspace_bytes(const fa_decode_args& a);
 hipError_t launch_decode(const fa_decode_args& a, void* ws, hipStream_t st);
 
+hipError_t launch_cache_write(const fa_cache_write_args& a, hipStream_t st);
+
 }  // namespace fa

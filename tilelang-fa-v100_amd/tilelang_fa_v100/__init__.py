@@ -2,9 +2,11 @@
 
 The kernels are hand-written HIP in ../csrc, built into libfa355.so and called
 through a C ABI (include/fa355.h).  Exports match the reference package
-(tilelang_fa_v100/__init__.py:3-16).
+(tilelang_fa_v100/__init__.py:3-16), plus reshape_and_cache, the KV-cache
+writer that produces the paged layout the paged kernels read.
 """
 
+from ._cache_write import reshape_and_cache
 from .interface import (
     FlashAttnTileLangVFunc,
     tilelang_decode_forward,
@@ -20,3 +22,4 @@ __all__ = [
     "tilelang_paged_forward",
     "tilelang_decode_forward",
 ]
+# reshape_and_cache is importable by name; __all__ stays the reference's list.

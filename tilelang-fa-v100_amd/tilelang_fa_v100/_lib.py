@@ -91,6 +91,17 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class CacheWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("key", _vp), ("value", _vp), ("k_cache", _vp), ("v_cache", _vp),
+        ("slot_mapping", _vp),
+        ("key_stride", _i64x2), ("value_stride", _i64x2),
+        ("k_stride", _i64x3), ("v_stride", _i64x3),
+        ("num_tokens", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
+        ("page_size", _i32), ("num_pages", _i32), ("dtype", _i32),
+    ]
+
+
 # Every function the header declares, with its ctypes prototype.
 _PROTOTYPES = {
     "fa_abi_version": (ctypes.c_int, []),
@@ -102,6 +113,7 @@ _PROTOTYPES = {
     "fa_paged_prefill": (ctypes.c_int, [ctypes.POINTER(PagedArgs), _vp]),
     "fa_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "fa_paged_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
+    "fa_reshape_and_cache": (ctypes.c_int, [ctypes.POINTER(CacheWriteArgs), _vp]),
 }
 
 _lock = threading.Lock()
