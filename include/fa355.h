@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FA355_ABI_VERSION 1
+#define FA355_ABI_VERSION 2
 
 typedef enum fa_status {
   FA_OK = 0,
@@ -59,6 +59,11 @@ typedef enum fa_dtype {
 /* Strides are in elements: {batch, seq, head}; head_dim is contiguous.     */
 /* Causal masking is bottom-right aligned: key j is visible to query i iff  */
 /* j <= i + seqlen_k - seqlen_q (tests/test_compare_ref.py:22 convention).  */
+/* Sliding window (FlashAttention-2 window_size, off = seqlen_k - seqlen_q),*/
+/* read only when has_window is non-zero (a zeroed struct has no window):   */
+/* key j is visible to query i iff j >= i + off - window_left (when         */
+/* window_left >= 0) and j <= i + off + window_right (when window_right     */
+/* >= 0); causal implies window_right = 0.  -1 means unbounded.             */
 /* A query row with no visible key gets out = 0 and lse = -inf.             */
 /* ------------------------------------------------------------------------ */
 typedef struct fa_fwd_args {
@@ -80,6 +85,9 @@ typedef struct fa_fwd_args {
   float softmax_scale;
   int32_t causal;
   int32_t dtype;       /* fa_dtype; q, k, v, out share it */
+  int32_t has_window;   /* 0: window_left / window_right are ignored */
+  int32_t window_left;  /* -1: unbounded */
+  int32_t window_right; /* -1: unbounded (0 implied when causal) */
 } fa_fwd_args;
 
 /* Replaces tilelang_forward_lse (_kernels_forward.py:188-193) + the launch at
@@ -117,6 +125,9 @@ typedef struct fa_bwd_args {
   int32_t causal;
   int32_t dtype;
   int32_t deterministic; /* accepted; the dQ reduction order is fixed per tile */
+  int32_t has_window;    /* as in fa_fwd_args */
+  int32_t window_left;
+  int32_t window_right;
 } fa_bwd_args;
 
 /* Replaces tilelang_backward (_kernels_backward.py:200-208). */

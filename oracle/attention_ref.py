@@ -32,18 +32,29 @@ def _expand_kv(k: torch.Tensor, heads: int) -> torch.Tensor:
     return k.repeat_interleave(g, dim=2) if g > 1 else k
 
 
-def dense_visible(sq: int, sk: int, causal: bool) -> torch.Tensor:
+def dense_visible(sq: int, sk: int, causal: bool, window=(-1, -1)) -> torch.Tensor:
     """Bool [sq, sk]: key j visible to query i.
 
     Causal is bottom-right aligned, j <= i + sk - sq: the reference's oracle
     `torch.tril(ones(M, N), diagonal=N - M)` (tests/test_compare_ref.py:21-23)
     and its kernel mask (_kernels_forward.py:135-144).
+    window = (left, right) follows FlashAttention-2's window_size, which the
+    reference's signature carries (interface.py:59-62) but ignores (:33):
+    j >= i + off - left when left >= 0, j <= i + off + right when right >= 0,
+    off = sk - sq; causal implies right = 0.
     """
-    if not causal:
-        return torch.ones(sq, sk, dtype=torch.bool)
     i = torch.arange(sq).unsqueeze(1)
     j = torch.arange(sk).unsqueeze(0)
-    return j <= i + (sk - sq)
+    off = sk - sq
+    left, right = window
+    if causal:
+        right = 0
+    vis = torch.ones(sq, sk, dtype=torch.bool)
+    if right >= 0:
+        vis &= j <= i + off + right
+    if left >= 0:
+        vis &= j >= i + off - left
+    return vis
 
 
 def masked_softmax_attention(q, k, v, visible, scale, dtype=torch.float32):
@@ -61,7 +72,7 @@ def masked_softmax_attention(q, k, v, visible, scale, dtype=torch.float32):
     return out, lse
 
 
-def dense_attention(q, k, v, scale=None, causal=False, dtype=torch.float32):
+def dense_attention(q, k, v, scale=None, causal=False, dtype=torch.float32, window=(-1, -1)):
     """softmax(scale * Q K^T + mask) V and its LSE.
 
     Follows tests/test_compare_ref.py:15-25 (math) and
@@ -73,7 +84,7 @@ def dense_attention(q, k, v, scale=None, causal=False, dtype=torch.float32):
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     ke, ve = _expand_kv(k, H), _expand_kv(v, H)
-    vis = dense_visible(Sq, Sk, causal)
+    vis = dense_visible(Sq, Sk, causal, window)
     outs, lses = [], []
     for b in range(B):
         o, l = masked_softmax_attention(q[b], ke[b], ve[b], vis, scale, dtype)
@@ -82,7 +93,8 @@ def dense_attention(q, k, v, scale=None, causal=False, dtype=torch.float32):
     return torch.stack(outs), torch.stack(lses)
 
 
-def dense_attention_backward(q, k, v, dout, scale=None, causal=False, dtype=torch.float32):
+def dense_attention_backward(q, k, v, dout, scale=None, causal=False, dtype=torch.float32,
+                             window=(-1, -1)):
     """Gradients of dense_attention w.r.t. q, k, v by the FlashAttention-2
     formulas the reference kernels implement:
       P = exp(scale*S - lse), rowdot = sum_d O*dO   (_kernels_backward.py:203)
@@ -98,7 +110,7 @@ def dense_attention_backward(q, k, v, dout, scale=None, causal=False, dtype=torc
         scale = 1.0 / math.sqrt(D)
     ke, ve = _expand_kv(k, H).to(dtype), _expand_kv(v, H).to(dtype)
     qf, dof = q.to(dtype), dout.to(dtype)
-    vis = dense_visible(Sq, Sk, causal)
+    vis = dense_visible(Sq, Sk, causal, window)
     dq = torch.zeros(B, Sq, H, D, dtype=dtype)
     dke = torch.zeros(B, Sk, H, D, dtype=dtype)
     dve = torch.zeros(B, Sk, H, D, dtype=dtype)

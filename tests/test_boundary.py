@@ -310,3 +310,14 @@ def test_cache_write_abi_rejects_bad_arguments():
     assert lib.fa_reshape_and_cache(ctypes.byref(a), None) == _lib.FA_E_UNSUPPORTED
     a.key = 0
     assert lib.fa_reshape_and_cache(ctypes.byref(a), None) == _lib.FA_E_INVALID
+
+
+def test_window_size_is_validated_before_launch():
+    q = torch.zeros(1, 4, 2, 64, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        fa.tilelang_flash_attn_func(q, q, q, window_size=(-2, 0))
+    with pytest.raises(ValueError):
+        fa.tilelang_flash_attn_func(q, q, q, window_size=(3,))
+    lib = _lib.load()
+    a = fwd_args(has_window=1, window_left=-5)
+    assert lib.fa_fwd(ctypes.byref(a), None) == _lib.FA_E_INVALID

@@ -111,3 +111,76 @@ def test_forward_is_deterministic():
     a = fa.tilelang_flash_attn_func(q, k, v, causal=True)
     b = fa.tilelang_flash_attn_func(q, k, v, causal=True)
     assert torch.equal(a, b)
+
+
+WINDOW_CASES = [
+    # (B, Sq, Sk, H, Hk, D, causal, window, dtype)
+    (1, 700, 700, 4, 2, 128, True, (130, -1), torch.float16),    # causal + left window
+    (2, 300, 520, 4, 4, 128, False, (64, 32), torch.float16),    # two-sided band, Sk > Sq
+    (1, 520, 300, 2, 2, 128, False, (-1, 0), torch.float16),     # right bound only, Sq > Sk
+    (1, 600, 600, 4, 4, 64, True, (17, -1), torch.float16),      # D = 64 kernels
+    (1, 333, 333, 2, 1, 64, False, (40, 300), torch.bfloat16),
+    (1, 257, 257, 2, 2, 256, True, (100, -1), torch.float16),    # D = 256 forward only
+]
+
+
+def _wids(c):
+    B, Sq, Sk, H, Hk, D, causal, w, dt = c
+    return f"{Sq}x{Sk}-D{D}-{'c' if causal else 'nc'}-w{w[0]}_{w[1]}-{str(dt)[6:]}"
+
+
+@pytest.mark.parametrize("case", WINDOW_CASES, ids=[_wids(c) for c in WINDOW_CASES])
+def test_sliding_window_forward_and_backward(case):
+    """window_size with FlashAttention-2 semantics (the reference ignores it)."""
+    B, Sq, Sk, H, Hk, D, causal, window, dt = case
+    g = torch.Generator().manual_seed(7)
+    q, k, v = randn(g, B, Sq, H, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt)
+    do = randn(g, B, Sq, H, D, dtype=dt)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out, lse, _ = fa.tilelang_flash_attn_func(qd, kd, vd, causal=causal, window_size=window,
+                                              return_attn_probs=True)
+    r_out, r_lse = ref.dense_attention(q, k, v, causal=causal, window=window)
+    assert_close(out, r_out)
+    assert_lse(lse, r_lse)
+    if D == 256:
+        return
+    out.backward(do.to(DEV))
+    r_dq, r_dk, r_dv = ref.dense_attention_backward(q, k, v, do, causal=causal, window=window)
+    assert_close(qd.grad, r_dq, what="dq")
+    assert_close(kd.grad, r_dk, what="dk")
+    assert_close(vd.grad, r_dv, what="dv")
+
+
+def test_default_window_is_full_attention():
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (randn(g, 1, 200, 2, 128).to(DEV) for _ in range(3))
+    a = fa.tilelang_flash_attn_func(q, k, v, causal=True)
+    b = fa.tilelang_flash_attn_func(q, k, v, causal=True, window_size=(-1, -1))
+    c = fa.tilelang_flash_attn_func(q, k, v, causal=True, window_size=(10**6, 5))
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+
+def test_sliding_window_bf16_gradients():
+    """bf16 band: forward to the elementwise bar, gradients by relative L2.
+
+    bf16 keeps 8 significant bits, and the backward's P and dS enter the
+    matrix products as bf16, so a key's dK / dV sums ~100 terms each carrying
+    ~2^-9 relative rounding; inside a narrow band P is large and single
+    elements can exceed atol 2e-3 / rtol 1e-2 (fp16 cases of the same shapes
+    meet it elementwise, see test_sliding_window_forward_and_backward).
+    """
+    g = torch.Generator().manual_seed(9)
+    B, Sq, Sk, H, Hk, D, window = 2, 300, 520, 4, 4, 128, (64, 32)
+    dt = torch.bfloat16
+    q, k, v = randn(g, B, Sq, H, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt)
+    do = randn(g, B, Sq, H, D, dtype=dt)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out, lse, _ = fa.tilelang_flash_attn_func(qd, kd, vd, window_size=window, return_attn_probs=True)
+    r_out, r_lse = ref.dense_attention(q, k, v, window=window)
+    assert_close(out, r_out)
+    assert_lse(lse, r_lse)
+    out.backward(do.to(DEV))
+    r = ref.dense_attention_backward(q, k, v, do, window=window)
+    for got, want, name in zip((qd.grad, kd.grad, vd.grad), r, ("dq", "dk", "dv")):
+        assert rel_l2(got, want) < 1e-2, name

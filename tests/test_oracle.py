@@ -245,7 +245,7 @@ def test_pair_counts_match_enumeration_and_survey_configs():
 # ------------------------------------------------------------------ planted mistakes
 
 def test_planted_top_left_causal_mask_is_caught(gold, monkeypatch):
-    def top_left(sq, sk, causal):
+    def top_left(sq, sk, causal, window=(-1, -1)):
         i = torch.arange(sq).unsqueeze(1)
         j = torch.arange(sk).unsqueeze(0)
         return j <= i if causal else torch.ones(sq, sk, dtype=torch.bool)
@@ -332,3 +332,51 @@ def test_planted_transposed_page_slot_is_caught(monkeypatch):
     monkeypatch.setattr(ref, "reshape_and_cache", bad)
     with pytest.raises(AssertionError):
         test_reshape_and_cache_round_trips_through_paged_rows()
+
+
+# ------------------------------------------------------------------ dense sliding window
+
+def test_dense_window_matches_enumeration():
+    """FlashAttention-2 window_size semantics, pair by pair."""
+    rng = np.random.default_rng(11)
+    for _ in range(60):
+        sq, sk = int(rng.integers(1, 9)), int(rng.integers(1, 9))
+        left, right = int(rng.integers(-1, 5)), int(rng.integers(-1, 5))
+        causal = bool(rng.integers(0, 2))
+        vis = ref.dense_visible(sq, sk, causal, (left, right))
+        off = sk - sq
+        r = 0 if causal else right
+        for i in range(sq):
+            for j in range(sk):
+                exp = (r < 0 or j <= i + off + r) and (left < 0 or j >= i + off - left)
+                assert bool(vis[i, j]) == exp, (sq, sk, left, right, causal, i, j)
+
+
+def test_dense_window_closed_forms():
+    g = torch.Generator().manual_seed(12)
+    q, k, v = (torch.randn(1, 9, 2, 8, generator=g, dtype=torch.float64) for _ in range(3))
+    # window (0, 0) with Sq == Sk: query i sees key i only -> out = v[i], lse = scaled score.
+    out, lse = ref.dense_attention(q, k, v, causal=False, window=(0, 0), dtype=torch.float64)
+    assert torch.equal(out, v)
+    s = (q * k).sum(-1).transpose(1, 2) / math.sqrt(8)
+    assert torch.allclose(lse, s, atol=1e-12)
+    # unbounded window = plain attention; causal ignores the right bound.
+    a, _ = ref.dense_attention(q, k, v, causal=True, window=(-1, 5), dtype=torch.float64)
+    b, _ = ref.dense_attention(q, k, v, causal=True, dtype=torch.float64)
+    assert torch.equal(a, b)
+    # left window >= Sk changes nothing.
+    a, _ = ref.dense_attention(q, k, v, causal=True, window=(9, -1), dtype=torch.float64)
+    assert torch.equal(a, b)
+
+
+def test_dense_window_backward_matches_autograd():
+    g = torch.Generator().manual_seed(13)
+    q, k, v, do = (torch.randn(1, 7, 2, 4, generator=g, dtype=torch.float64) for _ in range(4))
+    for causal, window in ((True, (2, -1)), (False, (1, 2)), (False, (-1, 0))):
+        qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+        out, _ = ref.dense_attention(qa, ka, va, causal=causal, window=window, dtype=torch.float64)
+        out.backward(do)
+        dq, dk, dv = ref.dense_attention_backward(q, k, v, do, causal=causal, window=window,
+                                                  dtype=torch.float64)
+        for got, want in ((dq, qa.grad), (dk, ka.grad), (dv, va.grad)):
+            assert torch.allclose(got, want, atol=1e-10)

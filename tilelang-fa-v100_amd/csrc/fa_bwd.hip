@@ -93,6 +93,8 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 }
 
 // ------------------------------------------------------------ main kernel
+// CAUSAL: causal or windowed (the band comes from the arguments); false: full
+// attention.
 template <class T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqacc,
                                                        const float* stats) {
@@ -115,7 +117,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
   const int bh = id / kvtiles;
   const int hk = bh % Hk, b = bh / Hk;
   const int kv0 = kt_idx * S::BKV;
-  const int off = Sk - Sq;  // key n visible to query i iff n <= i + off
+  const Band band = make_band(a);  // CAUSAL false: no band (full attention)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
@@ -167,9 +169,10 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
 
   // Query rows that can see any key of this tile.
-  const int q_begin = CAUSAL ? max(0, kv0 - off) : 0;
+  const int q_begin = CAUSAL ? band.first_row(kv0) : 0;
+  const int q_end = CAUSAL ? band.end_row(kv0 + S::BKV - 1, Sq) : Sq;
   const int it0 = q_begin / S::BQ;
-  const int it1 = (Sq + S::BQ - 1) / S::BQ;
+  const int it1 = (q_end + S::BQ - 1) / S::BQ;
   const int nit = max(it1 - it0, 0);
   const int wkv_last = min(kv0w + 31, Sk - 1);
 
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     if (more) load_q(t + 1);
 
     // Does this wave's key block see any of these query rows?
-    const bool active = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0w);
+    const bool active = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0w, kv0w + 31);
     const bool wvalid = kv0w < Sk;
     if (active && wvalid) {
       f32x16 s[S::NQT], dp[S::NQT];
@@ -259,7 +262,8 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
         }
       }
       // Masking is needed on the diagonal band and on a partial key block.
-      const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kv0w + 32 > Sk);
+      const bool need_mask = (CAUSAL && !band.all(i0, i0 + S::BQ - 1, kv0w, wkv_last)) ||
+                             (kv0w + 32 > Sk);
 #pragma unroll
       for (int qt = 0; qt < S::NQT; ++qt)
 #pragma unroll
@@ -273,7 +277,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
             float p = fast_exp2(fmaf(s[qt][i], scale_log2, -l4[r]));
             if (need_mask) {
               const int qi = i0 + qb + r;
-              const bool vis = (my_kv < Sk) && (!CAUSAL || my_kv <= qi + off);
+              const bool vis = (my_kv < Sk) && (!CAUSAL || band.in(qi, my_kv));
               p = vis ? p : 0.f;
             }
             s[qt][i] = p;                       // P
@@ -326,7 +330,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
 
     // dQ[i0 + q][d] += sum_k dS[q][k] K[k][d] over this workgroup's 128 keys.
     {
-      const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
+      const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
       if (any) {
         float* dqb = dqacc + ((int64_t)b * H + h) * Sq * D;  // [B, H, Sq, D]
         const int64_t qstride = D;
@@ -421,13 +425,15 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  const Band band = make_band(a);
+  const bool banded = band.wl >= 0 || band.wr >= 0;
   if constexpr (D == 128) {
     using S2 = BwdShapeD128<kBwdKB>;
     const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
-    } else if (a.causal)
+    } else if (banded)
       hipLaunchKernelGGL((bwd_main_d128_kernel<T, true, kBwdKB>), grid, dim3(64 * S2::NW), 0, st,
                          a, dqacc, stats);
     else
@@ -438,7 +444,7 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
-    } else if (a.causal)
+    } else if (banded)
       hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc, stats);
     else
       hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc, stats);

@@ -55,6 +55,7 @@ struct BwdShapeD128 {
 // Key blocks per wave used by the launcher.
 constexpr int kBwdKB = 1;
 
+// CAUSAL: causal or windowed (band from the arguments); false: full attention.
 template <class T, bool CAUSAL, int KB>
 __global__ __launch_bounds__(64 * BwdShapeD128<KB>::NW, BwdShapeD128<KB>::WPE)
 void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
@@ -75,7 +76,10 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   const int bh = th.bh;
   const int hk = bh % Hk, b = bh / Hk;
   const int kv0 = kt_idx * S::BKV;
-  const int off = Sk - Sq;  // key n visible to query i iff n <= i + off
+  // Visible pairs: CAUSAL (causal or windowed) takes the band from the
+  // arguments; otherwise every (query, key) pair inside the bounds.
+  const Band band = make_band(a);
+  const int off = band.off;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
@@ -145,9 +149,10 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) dk[kb][dt][i] = dv[kb][dt][i] = 0.f;
 
-  const int q_begin = CAUSAL ? max(0, kv0 - off) : 0;
+  const int q_begin = CAUSAL ? band.first_row(kv0) : 0;
+  const int q_end = CAUSAL ? band.end_row(kv0 + S::BKV - 1, Sq) : Sq;
   const int it0 = q_begin / S::BQ;
-  const int it1 = (Sq + S::BQ - 1) / S::BQ;
+  const int it1 = (q_end + S::BQ - 1) / S::BQ;
   const int nit = max(it1 - it0, 0);
   const int ntot = nit * G;
   const int64_t head_rows = (int64_t)b * H + hk * G;  // (b, first query head) row block
@@ -205,7 +210,8 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     const int i0 = it * S::BQ;
     // Key block 0 has the smallest keys: if it sees none of the tile's
     // queries (or lies past Sk), no block of the wave does.
-    const bool active = (!CAUSAL || (i0 + S::BQ - 1 + off >= kvb(0))) && kvb(0) < Sk;
+    const bool active =
+        (!CAUSAL || band.any(i0, i0 + S::BQ - 1, kvb(0), kvb(KB - 1) + 31)) && kvb(0) < Sk;
     if (active) {
       f32x16 s[KB], dp[KB];
 #pragma unroll
@@ -233,8 +239,8 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
         const int kvw = kvb(kb);
         const int my_kv = kvw + lr;
         const int wkv_last = min(kvw + 31, Sk - 1);
-        const bool need_mask = (CAUSAL && (i0 + off < wkv_last)) || (kvw + 32 > Sk) ||
-                               (i0 + S::BQ > Sq);
+        const bool need_mask = (CAUSAL && !band.all(i0, i0 + S::BQ - 1, kvw, wkv_last)) ||
+                               (kvw + 32 > Sk) || (i0 + S::BQ > Sq);
         // P = exp2(S·scale·log2e − lse2), dS = P (dP − rowdot).  Element
         // (g, r) is query i0 + 8g + 4lh + r; on masked tiles it sees key
         // my_kv iff c = 8g + r lies in [t_lo, t_hi); masked elements get
@@ -243,8 +249,11 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
         auto softmax = [&](auto masked) {
           constexpr bool kMasked = decltype(masked)::value;
           const int rel = i0 + 4 * lh;
-          const int t_lo = CAUSAL ? my_kv - off - rel : -0x40000000;
-          const int t_hi = (my_kv < Sk) ? Sq - rel : -0x40000000;
+          // j <= i + off + wr  <=>  c >= j - off - wr - rel;
+          // j >= i + off - wl  <=>  c <= j - off + wl - rel.
+          const int t_lo = (CAUSAL && band.wr >= 0) ? my_kv - off - band.wr - rel : -0x40000000;
+          int t_hi = (my_kv < Sk) ? Sq - rel : -0x40000000;
+          if (CAUSAL && band.wl >= 0) t_hi = min(t_hi, my_kv - off + band.wl - rel + 1);
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int qb4 = 8 * g + 4 * lh;
@@ -315,7 +324,7 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   // tile whose dSᵀ is complete in dsb (waves 0 .. DQW-1, one d tile each).
   auto dq_step = [&](int h_rel, int it, const char* dsb) {
     const int i0 = it * S::BQ;
-    const bool any = !CAUSAL || (i0 + S::BQ - 1 + off >= kv0);
+    const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
     if (wave < S::DQW && any) {
       const int dt = wave;
       f32x16 acc;

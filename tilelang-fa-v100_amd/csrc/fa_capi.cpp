@@ -93,6 +93,8 @@ static int check_fwd(const fa_fwd_args* a) {
   if (!strides_ok(a->q_stride, 3) || !strides_ok(a->k_stride, 3) ||
       !strides_ok(a->v_stride, 3) || !strides_ok(a->o_stride, 3))
     return fail(FA_E_UNSUPPORTED, "fa_fwd: strides must be non-negative multiples of 8");
+  if (a->has_window && (a->window_left < -1 || a->window_right < -1))
+    return fail(FA_E_INVALID, "fa_fwd: window sizes must be >= -1");
   const int64_t tiles = ((int64_t)a->seqlen_q + 127) / 128 * a->num_heads * a->batch;
   if (tiles > kIntMax) return fail(FA_E_UNSUPPORTED, "fa_fwd: problem too large");
   return ok();
@@ -133,6 +135,8 @@ static int check_bwd(const fa_bwd_args* a) {
     if (s[1] >= kMaxRowStride)
       return fail(FA_E_UNSUPPORTED, "fa_bwd: sequence strides must be below 2^26 elements");
   }
+  if (a->has_window && (a->window_left < -1 || a->window_right < -1))
+    return fail(FA_E_INVALID, "fa_bwd: window sizes must be >= -1");
   const int64_t tiles = ((int64_t)a->seqlen_k + 127) / 128 * a->num_heads_k * a->batch;
   const int64_t rows = (int64_t)a->batch * a->seqlen_q * a->num_heads;
   if (tiles > kIntMax || rows / 16 > kIntMax)

@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fa355.h"
+
 namespace fa {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -138,6 +140,36 @@ __device__ __forceinline__ u32x2 ld8(const void* p) {
 }
 __device__ __forceinline__ void st8(void* p, u32x2 v) {
   *reinterpret_cast<u32x2*>(p) = v;
+}
+
+// Visible (query i, key j) pairs of the dense paths: j <= i + off + wr when
+// wr >= 0 and j >= i + off - wl when wl >= 0 (FlashAttention-2 window_size,
+// causal is wr = 0), off = Sk - Sq.  Row / key bounds are checked separately.
+struct Band {
+  int off, wl, wr;
+  // Some pair with i in [i0, i1] and j in [j0, j1] is inside the band.
+  __device__ bool any(int i0, int i1, int j0, int j1) const {
+    return (wr < 0 || j0 <= i1 + off + wr) && (wl < 0 || j1 >= i0 + off - wl);
+  }
+  // Every such pair is inside the band.
+  __device__ bool all(int i0, int i1, int j0, int j1) const {
+    return (wr < 0 || j1 <= i0 + off + wr) && (wl < 0 || j0 >= i1 + off - wl);
+  }
+  __device__ bool in(int i, int j) const {
+    return (wr < 0 || j <= i + off + wr) && (wl < 0 || j >= i + off - wl);
+  }
+  // Query rows [first, end) that see any key in [j0, j1], clipped to [0, sq).
+  __device__ int first_row(int j0) const { return wr >= 0 ? max(0, j0 - off - wr) : 0; }
+  __device__ int end_row(int j1, int sq) const {
+    return wl >= 0 ? min(sq, max(j1 - off + wl + 1, 0)) : sq;
+  }
+};
+
+template <class Args>
+__device__ __host__ __forceinline__ Band make_band(const Args& a) {
+  const int wl = a.has_window ? a.window_left : -1;
+  const int wr = a.causal ? 0 : (a.has_window ? a.window_right : -1);
+  return Band{a.seqlen_k - a.seqlen_q, wl, wr};
 }
 
 // Instruction-scheduling hint for a loop of N steps that each issue L LDS

@@ -24,11 +24,13 @@ struct DenseRows {
   const uint16_t* v;
   int64_t qs, os, ks, vs;  // per-row (sequence) strides, elements
   int nrows, sk, off;      // off = seqlen_k - seqlen_q
-  bool causal, has_lse;
+  int wl, wr;              // window bounds (-1: unbounded); causal is wr = 0
+  bool has_lse;
 
-  __device__ int kv_lo(int) const { return 0; }
+  // Row r sees keys [r + off - wl, r + off + wr] within [0, sk).
+  __device__ int kv_lo(int r) const { return wl >= 0 ? min(max(r + off - wl, 0), sk) : 0; }
   __device__ int kv_hi(int r) const {
-    return causal ? min(max(r + off + 1, 0), sk) : sk;
+    return wr >= 0 ? min(max(r + off + wr + 1, 0), sk) : sk;
   }
   __device__ const uint16_t* q_ptr(int r) const { return q + r * qs; }
   __device__ uint16_t* o_ptr(int r) const { return o + r * os; }
@@ -67,7 +69,9 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
   }
 }
 
-template <class T, int D, bool CAUSAL>
+// BANDED: causal or windowed (row key ranges move with the row); used for
+// the tile order only, the masks come from the arguments.
+template <class T, int D, bool BANDED>
 __global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
 void fwd_dense_kernel(fa_fwd_args a) {
   using C = FwdKernelCfg<D>;
@@ -77,7 +81,7 @@ void fwd_dense_kernel(fa_fwd_args a) {
   const int h = bh % a.num_heads;
   const int b = bh / a.num_heads;
   // Heaviest causal tiles (largest query index) first.
-  const int qt = CAUSAL ? qtiles - 1 - th.rank : th.rank;
+  const int qt = BANDED ? qtiles - 1 - th.rank : th.rank;
   const int hk = h / (a.num_heads / a.num_heads_k);
 
   DenseRows P;
@@ -93,7 +97,9 @@ void fwd_dense_kernel(fa_fwd_args a) {
   P.nrows = a.seqlen_q;
   P.sk = a.seqlen_k;
   P.off = a.seqlen_k - a.seqlen_q;
-  P.causal = CAUSAL;
+  const Band band = make_band(a);
+  P.wl = band.wl;
+  P.wr = band.wr;
   P.has_lse = a.lse != nullptr;
   run_fwd_tile<T, D>(P, qt * C::BM, a.softmax_scale);
 }
@@ -254,7 +260,8 @@ static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   using C = FwdKernelCfg<D>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
-  if (a.causal)
+  const Band band = make_band(a);
+  if (band.wl >= 0 || band.wr >= 0)
     hipLaunchKernelGGL((fwd_dense_kernel<T, D, true>), grid, dim3(C::THREADS), 0, st, a);
   else
     hipLaunchKernelGGL((fwd_dense_kernel<T, D, false>), grid, dim3(C::THREADS), 0, st, a);

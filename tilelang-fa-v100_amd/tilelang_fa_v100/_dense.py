@@ -33,7 +33,20 @@ def check_shapes(q, k, v):
     return B, Sq, k.shape[1], H, Hk, D
 
 
-def forward(q, k, v, softmax_scale: float, causal: bool):
+def window_bounds(window_size) -> tuple:
+    """(left, right) of a FlashAttention-2 window_size; -1 = unbounded."""
+    if window_size is None:
+        return -1, -1
+    try:
+        left, right = (int(x) for x in window_size)
+    except (TypeError, ValueError):
+        raise ValueError(f"window_size must be a pair of ints, got {window_size!r}") from None
+    if left < -1 or right < -1:
+        raise ValueError(f"window_size entries must be >= -1, got {window_size!r}")
+    return left, right
+
+
+def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1)):
     """Returns (out [B,Sq,H,D], lse [B,H,Sq] fp32)."""
     B, Sq, Sk, H, Hk, D = check_shapes(q, k, v)
     q, k, v = rows_ready(q), rows_ready(k), rows_ready(v)
@@ -50,13 +63,16 @@ def forward(q, k, v, softmax_scale: float, causal: bool):
     a.softmax_scale = float(softmax_scale)
     a.causal = int(bool(causal))
     a.dtype = _lib.dtype_code(q.dtype)
+    a.has_window = int(tuple(window) != (-1, -1))
+    a.window_left, a.window_right = window
     lib = _lib.load()
     with torch.cuda.device(q.device):
         _lib.check(lib.fa_fwd(ctypes.byref(a), _lib.stream_handle(q.device)), "fa_fwd")
     return out, lse
 
 
-def bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic):
+def bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic,
+             window=(-1, -1)):
     B, Sq, Sk, H, Hk, D = check_shapes(q, k, v)
     a = _lib.BwdArgs()
     a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
@@ -71,11 +87,13 @@ def bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, determi
     a.causal = int(bool(causal))
     a.dtype = _lib.dtype_code(q.dtype)
     a.deterministic = int(bool(deterministic))
+    a.has_window = int(tuple(window) != (-1, -1))
+    a.window_left, a.window_right = window
     return a
 
 
 def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
-             deterministic: bool = False):
+             deterministic: bool = False, window=(-1, -1)):
     """Returns (dq, dk, dv), each contiguous [B, S, H, D] in q's dtype."""
     if q.shape[-1] not in (64, 128):
         raise NotImplementedError(f"backward for head_dim {q.shape[-1]} is not implemented "
@@ -87,7 +105,8 @@ def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
     dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-    a = bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic)
+    a = bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic,
+                 window)
     lib = _lib.load()
     nbytes = lib.fa_bwd_workspace_bytes(ctypes.byref(a))
     if nbytes == 0:

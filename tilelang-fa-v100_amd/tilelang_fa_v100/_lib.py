@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 
 LIB_NAME = "libfa355.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FA_OK = 0
 FA_E_INVALID = -1
@@ -44,6 +44,7 @@ class FwdArgs(ctypes.Structure):
         ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32),
         ("num_heads", _i32), ("num_heads_k", _i32), ("head_dim", _i32),
         ("softmax_scale", _f32), ("causal", _i32), ("dtype", _i32),
+        ("has_window", _i32), ("window_left", _i32), ("window_right", _i32),
     ]
 
 
@@ -57,7 +58,8 @@ class BwdArgs(ctypes.Structure):
         ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32),
         ("num_heads", _i32), ("num_heads_k", _i32), ("head_dim", _i32),
         ("softmax_scale", _f32), ("causal", _i32), ("dtype", _i32),
-        ("deterministic", _i32),
+        ("deterministic", _i32), ("has_window", _i32), ("window_left", _i32),
+        ("window_right", _i32),
     ]
 
 

@@ -14,7 +14,10 @@ limitation):
   * dense K/V may have fewer heads than Q (GQA, contiguous head groups);
   * a query row that sees no key gets out = 0 and lse = -inf (the reference
     produces NaN);
-  * window_size is accepted and ignored, as in the reference (:33).
+  * window_size is honoured with FlashAttention-2 semantics (key j visible to
+    query i iff i + off - left <= j <= i + off + right, off = Sk - Sq, -1 =
+    unbounded, causal implies right = 0); the reference parses it and then
+    ignores it (:33).  The default (-1, -1) is identical.
 """
 from __future__ import annotations
 
@@ -46,9 +49,11 @@ class FlashAttnTileLangVFunc(torch.autograd.Function):
             require_cuda(t, name)
         require_same({"q": q, "k": k, "v": v}, "device")
         scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
-        out, lse = _dense.forward(q, k, v, scale, causal)
+        window = _dense.window_bounds(window_size)
+        out, lse = _dense.forward(q, k, v, scale, causal, window)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.causal = bool(causal)
+        ctx.window = window
         ctx.softmax_scale = float(scale)
         ctx.deterministic = bool(deterministic)
         if return_softmax:
@@ -59,7 +64,7 @@ class FlashAttnTileLangVFunc(torch.autograd.Function):
     def backward(ctx, dout, *args):
         q, k, v, out, lse = ctx.saved_tensors
         dq, dk, dv = _dense.backward(q, k, v, out, dout, lse, ctx.softmax_scale,
-                                     ctx.causal, ctx.deterministic)
+                                     ctx.causal, ctx.deterministic, ctx.window)
         return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
@@ -73,6 +78,7 @@ def tilelang_flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None,
         q: [B, Sq, H, D]; k, v: [B, Sk, Hk, D] with H % Hk == 0.
         causal: bottom-right aligned causal mask (key j visible to query i
             iff j <= i + Sk - Sq).
+        window_size: (left, right) sliding window, -1 = unbounded.
         softmax_scale: default 1/sqrt(D).
         return_attn_probs: return (out, lse [B, H, Sq] fp32, None).
     Returns:
