@@ -120,7 +120,7 @@ typedef struct fa_bwd_args {
   int32_t seqlen_k;
   int32_t num_heads;
   int32_t num_heads_k; /* num_heads % num_heads_k == 0 (GQA) */
-  int32_t head_dim;
+  int32_t head_dim;    /* 64, 128 or 256 */
   float softmax_scale;
   int32_t causal;
   int32_t dtype;

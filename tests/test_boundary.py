@@ -124,7 +124,7 @@ def test_bwd_workspace_size_and_checks():
     # workspace missing / too small is rejected before any launch
     assert lib.fa_bwd(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE
     assert lib.fa_bwd(ctypes.byref(a), 0x4000, 16, None) == _lib.FA_E_WORKSPACE
-    assert lib.fa_bwd(ctypes.byref(bwd_args(head_dim=256)), 0x4000, 1 << 40, None) == \
+    assert lib.fa_bwd(ctypes.byref(bwd_args(head_dim=96)), 0x4000, 1 << 40, None) == \
         _lib.FA_E_UNSUPPORTED
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(bwd_args(lse=None))) == 0
 

@@ -77,6 +77,10 @@ BWD_CASES = [
     (1, 300, 500, 4, 2, 128, True, torch.bfloat16),      # Sk > Sq, GQA, bf16
     (1, 500, 300, 2, 2, 128, True, torch.float16),       # Sq > Sk: empty rows
     (2, 130, 130, 8, 1, 64, True, torch.float16),        # MQA
+    (1, 300, 300, 4, 4, 256, True, torch.float16),       # D = 256
+    (2, 200, 333, 4, 2, 256, False, torch.bfloat16),     # D = 256, Sk > Sq, GQA
+    (1, 500, 260, 2, 2, 256, True, torch.float16),       # D = 256, Sq > Sk
+    (1, 64, 77, 2, 1, 256, False, torch.float16),        # D = 256, one partial key tile
 ]
 
 
@@ -120,7 +124,8 @@ WINDOW_CASES = [
     (1, 520, 300, 2, 2, 128, False, (-1, 0), torch.float16),     # right bound only, Sq > Sk
     (1, 600, 600, 4, 4, 64, True, (17, -1), torch.float16),      # D = 64 kernels
     (1, 333, 333, 2, 1, 64, False, (40, 300), torch.bfloat16),
-    (1, 257, 257, 2, 2, 256, True, (100, -1), torch.float16),    # D = 256 forward only
+    (1, 257, 257, 2, 2, 256, True, (100, -1), torch.float16),    # D = 256
+    (1, 300, 400, 2, 2, 256, False, (50, 70), torch.float16),
 ]
 
 
@@ -142,8 +147,6 @@ def test_sliding_window_forward_and_backward(case):
     r_out, r_lse = ref.dense_attention(q, k, v, causal=causal, window=window)
     assert_close(out, r_out)
     assert_lse(lse, r_lse)
-    if D == 256:
-        return
     out.backward(do.to(DEV))
     r_dq, r_dk, r_dv = ref.dense_attention_backward(q, k, v, do, causal=causal, window=window)
     assert_close(qd.grad, r_dq, what="dq")

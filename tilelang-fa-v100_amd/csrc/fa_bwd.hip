@@ -21,9 +21,9 @@
 //                       loops over the 64-row query tiles of every query
 //                       head that shares the KV head (GQA).  K and V of the wave stay in registers,
 //                       K^T of the workgroup stays in LDS.
-//   bwd_main_d128_kernel  head_dim 128 variant (fa_bwd_d128.h).
+//   bwd_main_mfma_kernel  head_dim 128 / 256 variant (fa_bwd_mfma.h).
 //   bwd_dq_convert      dQ = scale * acc, cast to the input dtype.
-#include "fa_bwd_d128.h"
+#include "fa_bwd_mfma.h"
 #include "fa_common.h"
 #include "fa_internal.h"
 
@@ -93,12 +93,13 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 }
 
 // ------------------------------------------------------------ main kernel
-// CAUSAL: causal or windowed (the band comes from the arguments); false: full
-// attention.
-template <class T, int D, bool CAUSAL>
+// MODE (MaskMode): full attention, causal, or a window band from the
+// arguments.
+template <class T, int D, int MODE>
 __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqacc,
                                                        const float* stats) {
   using S = BwdShape<D>;
+  constexpr bool CAUSAL = MODE != kMaskNone;  // some (query, key) pairs are outside the band
   __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
   __shared__ __attribute__((aligned(16))) float lse_s[S::BQ];
   __shared__ __attribute__((aligned(16))) float di_s[S::BQ];
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
   const int bh = id / kvtiles;
   const int hk = bh % Hk, b = bh / Hk;
   const int kv0 = kt_idx * S::BKV;
-  const Band band = make_band(a);  // CAUSAL false: no band (full attention)
+  const Band band = mode_band<MODE>(a);  // kMaskNone: no band (full attention)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
@@ -416,7 +417,6 @@ size_t bwd_workspace_bytes(const fa_bwd_args& a) {
 
 template <class T, int D>
 static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
-  using S = BwdShape<D>;
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
   float* dqacc = static_cast<float*>(ws);
   float* stats = dqacc + rows * D;  // [B*H][2][Sq]
@@ -425,29 +425,38 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const Band band = make_band(a);
-  const bool banded = band.wl >= 0 || band.wr >= 0;
-  if constexpr (D == 128) {
-    using S2 = BwdShapeD128<kBwdKB>;
+  const int mode = mask_mode(a);
+  if constexpr (D >= 128) {
+    constexpr int KB = D == 128 ? kBwdKB : 1;
+    using S2 = BwdShapeMfma<D, KB>;
     const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
-    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
+    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S2::NW);
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
-    } else if (banded)
-      hipLaunchKernelGGL((bwd_main_d128_kernel<T, true, kBwdKB>), grid, dim3(64 * S2::NW), 0, st,
-                         a, dqacc, stats);
+    } else if (mode == kMaskCausal)
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal, KB>), grid, block, 0, st, a,
+                         dqacc, stats);
+    else if (mode == kMaskBand)
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand, KB>), grid, block, 0, st, a,
+                         dqacc, stats);
     else
-      hipLaunchKernelGGL((bwd_main_d128_kernel<T, false, kBwdKB>), grid, dim3(64 * S2::NW), 0,
-                         st, a, dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone, KB>), grid, block, 0, st, a,
+                         dqacc, stats);
   } else {
+    using S = BwdShape<D>;
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
     if (kvtiles == 0) {
       // No keys: dQ stays zero; dK / dV are empty.
-    } else if (banded)
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, true>), grid, dim3(256), 0, st, a, dqacc, stats);
+    } else if (mode == kMaskCausal)
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskCausal>), grid, dim3(256), 0, st, a, dqacc,
+                         stats);
+    else if (mode == kMaskBand)
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskBand>), grid, dim3(256), 0, st, a, dqacc,
+                         stats);
     else
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, false>), grid, dim3(256), 0, st, a, dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskNone>), grid, dim3(256), 0, st, a, dqacc,
+                         stats);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -460,6 +469,7 @@ static hipError_t launch_bwd_t(const fa_bwd_args& a, void* ws, hipStream_t st) {
   switch (a.head_dim) {
     case 64: return launch_bwd_d<T, 64>(a, ws, st);
     case 128: return launch_bwd_d<T, 128>(a, ws, st);
+    case 256: return launch_bwd_d<T, 256>(a, ws, st);
   }
   return hipErrorInvalidValue;
 }

@@ -1,16 +1,19 @@
-// Attention backward main kernel for head_dim 128 on gfx950.
+// Attention backward main kernel for head_dim 128 and 256 on gfx950.
 //
 // Same mathematics as bwd_main_kernel (fa_bwd.hip): per (key tile, query
 // tile) the 5 products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS and
 // dQ += dS K, with P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot).
 // Layout, for the gfx950 memory instructions:
-//  * 256 keys per workgroup: NW = 8 / KB waves, each owning KB blocks of 32
-//    keys.  The fp32 atomics that reduce dQ across key tiles then cover 256
-//    keys each, and every Q / dO tile fetched into LDS serves 256 keys.
-//    With KB = 2 (4 waves, one per SIMD) a wave has 512 registers, holds
-//    dK / dV of 64 keys, and every Q / dO operand it reads from LDS feeds
-//    the products of both its key blocks.
-//  * The workgroup's K tile (256 x 256 B) is copied once HBM -> LDS with
+//  * D = 128: 256 keys per workgroup, NW = 8 / KB waves, each owning KB
+//    blocks of 32 keys.  The fp32 atomics that reduce dQ across key tiles
+//    then cover 256 keys each, and every Q / dO tile fetched into LDS serves
+//    256 keys.  With KB = 2 (4 waves, one per SIMD) a wave has 512
+//    registers, holds dK / dV of 64 keys, and every Q / dO operand it reads
+//    from LDS feeds the products of both its key blocks.
+//  * D = 256: 128 keys per workgroup, 4 waves x 32 keys, one wave per SIMD
+//    (dK / dV of 32 keys x 256 d take 256 registers); rows are 512 bytes,
+//    and each wave computes two 32-wide d tiles of dQ.
+//  * The workgroup's K tile (BKV x 2D bytes) is copied once HBM -> LDS with
 //    global_load_lds_dwordx4 and serves as the B operand of S (row reads)
 //    and of dQ (transpose reads).  V rows of each wave stay in registers.
 //  * Q and dO tiles (32 rows) are DMA'd through buffer resources
@@ -20,13 +23,13 @@
 //  * dSᵀ goes to LDS (double-buffered) with 8-byte stores (its 8-byte
 //    pieces XOR-swizzled by row so both the stores and the transpose reads
 //    are conflict free) and is read back transposed as the A operand of dQ.
-//    Four waves each compute the 32 x 32 dQ block of one 32-wide d tile over
+//    Four waves each compute the 32 x 32 dQ blocks of their d tiles over
 //    all keys of the workgroup, one iteration later (after the single
 //    barrier of the next iteration), so the dQ products overlap the S / dP
 //    products of the next tile, and add it to the fp32 accumulator with
 //    buffer atomics.
-//  * 256-byte K / Q / dO rows use the 16-byte-chunk swizzle of
-//    fa_fwd_d128.h.
+//  * K / Q / dO rows use the 16-byte-chunk swizzle of fa_fwd_d128.h on the
+//    low four chunk bits (within each 256-byte half of a 512-byte row).
 #pragma once
 
 #include "fa355.h"
@@ -35,31 +38,38 @@
 
 namespace fa {
 
-template <int KB>
-struct BwdShapeD128 {
-  static constexpr int D = 128;
-  static constexpr int NW = 8 / KB;         // waves per workgroup
-  static constexpr int BKV = 32 * KB * NW;  // 256 keys per workgroup
+template <int D_, int KB>
+struct BwdShapeMfma {
+  static constexpr int D = D_;
+  static constexpr int NW = D == 128 ? 8 / KB : 4;  // waves per workgroup
+  static constexpr int BKV = 32 * KB * NW;  // keys per workgroup: 256 (D=128), 128 (D=256)
   static constexpr int BQ = 32;             // query rows per iteration
-  static constexpr int ROWB = 256;
+  static constexpr int ROWB = 2 * D;        // bytes per K / Q / dO row
+  static constexpr int CPR = D / 8;         // 16-byte chunks per row
+  static constexpr int RPB = 1024 / ROWB;   // rows per 1 KB DMA block
   static constexpr int K_BYTES = BKV * ROWB;  // 64 KB
-  static constexpr int QT_BYTES = BQ * ROWB;  // 8 KB
+  static constexpr int QT_BYTES = BQ * ROWB;  // 8 or 16 KB
+  static constexpr int QT_BLOCKS = QT_BYTES / 1024;
   static constexpr int DS_ROWB = BQ * 2;      // 64 B per dSᵀ row
-  static constexpr int DS_BYTES = BKV * DS_ROWB;  // 16 KB, double-buffered
-  static constexpr int DQW = D / 32;          // waves computing dQ (one d tile each)
+  static constexpr int DS_BYTES = BKV * DS_ROWB;  // double-buffered
+  static constexpr int DQT = D / 32;          // 32-wide d tiles of dQ
+  static constexpr int DQW = NW < DQT ? NW : DQT;  // waves computing dQ
+  static constexpr int DTW = DQT / DQW;       // d tiles per dQ wave
   static constexpr int WPE = NW / 4;          // waves per SIMD
-  static_assert(KB == 1 || KB == 2, "key blocks per wave");
-  static_assert(NW >= DQW, "dQ split");
+  static_assert(D == 128 || D == 256, "head_dim");
+  static_assert(KB == 1 || (KB == 2 && D == 128), "key blocks per wave");
+  static_assert(QT_BLOCKS % NW == 0 && (K_BYTES / 1024) % NW == 0, "DMA split");
 };
 
 // Key blocks per wave used by the launcher.
 constexpr int kBwdKB = 1;
 
-// CAUSAL: causal or windowed (band from the arguments); false: full attention.
-template <class T, bool CAUSAL, int KB>
-__global__ __launch_bounds__(64 * BwdShapeD128<KB>::NW, BwdShapeD128<KB>::WPE)
-void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
-  using S = BwdShapeD128<KB>;
+// MODE (MaskMode): full attention, causal, or a window band from the arguments.
+template <class T, int D_, int MODE, int KB>
+__global__ __launch_bounds__((64 * BwdShapeMfma<D_, KB>::NW), (BwdShapeMfma<D_, KB>::WPE))
+void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
+  using S = BwdShapeMfma<D_, KB>;
+  constexpr bool CAUSAL = MODE != kMaskNone;  // some (query, key) pairs are outside the band
   constexpr int D = S::D;
   __shared__ __attribute__((aligned(16))) char Ks[S::K_BYTES];
   __shared__ __attribute__((aligned(16))) char Q0[S::QT_BYTES], O0[S::QT_BYTES];
@@ -76,9 +86,9 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   const int bh = th.bh;
   const int hk = bh % Hk, b = bh / Hk;
   const int kv0 = kt_idx * S::BKV;
-  // Visible pairs: CAUSAL (causal or windowed) takes the band from the
-  // arguments; otherwise every (query, key) pair inside the bounds.
-  const Band band = make_band(a);
+  // Visible pairs: the band of MODE; with kMaskNone every (query, key) pair
+  // inside the bounds.
+  const Band band = mode_band<MODE>(a);
   const int off = band.off;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -91,13 +101,14 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
 
-  // ---- K tile -> LDS: 64 blocks of 1 KB (4 rows each); wave w loads
-  // blocks 8 KB w .. 8 KB w + 8 KB - 1 = its own key rows.
+  // ---- K tile -> LDS: 64 blocks of 1 KB (RPB rows each); wave w loads the
+  // blocks of its own key rows.
+  constexpr int KBPW = S::K_BYTES / 1024 / S::NW;
 #pragma unroll
-  for (int ii = 0; ii < 8 * KB; ++ii) {
-    const int blk = 8 * KB * wave + ii;
-    const int r = 4 * blk + (lane >> 4);
-    const int c = (lane & 15) ^ swz_chunk(r);
+  for (int ii = 0; ii < KBPW; ++ii) {
+    const int blk = KBPW * wave + ii;
+    const int r = S::RPB * blk + lane / S::CPR;
+    const int c = (lane % S::CPR) ^ swz_chunk(r);
     const int n = min(kv0 + r, Sk - 1);
     load_lds16(kg + (int64_t)n * a.k_stride[1] + 8 * c, Ks + blk * 1024);
   }
@@ -157,16 +168,16 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   const int ntot = nit * G;
   const int64_t head_rows = (int64_t)b * H + hk * G;  // (b, first query head) row block
 
-  // Q / dO tile loader: 32 rows = 8 blocks of 1 KB; each wave loads 8 / NW
-  // of them.  Lane l of block blk holds row 4 blk + l/16, stored chunk l%16
-  // (logical chunk (l%16) ^ swz(row)); its byte offset from the tile's first
-  // row is fixed.
-  constexpr int BPW = 8 / S::NW;
+  // Q / dO tile loader: 32 rows = QT_BLOCKS blocks of 1 KB; each wave loads
+  // QT_BLOCKS / NW of them.  Lane l of block blk holds row RPB blk + l/CPR,
+  // stored chunk l%CPR (logical chunk (l%CPR) ^ swz(row)); its byte offset
+  // from the tile's first row is fixed.
+  constexpr int BPW = S::QT_BLOCKS / S::NW;
   uint32_t q_loff[BPW], o_loff[BPW];
 #pragma unroll
   for (int ii = 0; ii < BPW; ++ii) {
-    const int r = 4 * (BPW * wave + ii) + (lane >> 4);
-    const uint32_t c = (lane & 15) ^ swz_chunk(r);
+    const int r = S::RPB * (BPW * wave + ii) + lane / S::CPR;
+    const uint32_t c = (lane % S::CPR) ^ swz_chunk(r);
     q_loff[ii] = 2u * (r * (uint32_t)a.q_stride[1] + 8 * c);
     o_loff[ii] = 2u * (r * (uint32_t)a.do_stride[1] + 8 * c);
   }
@@ -208,10 +219,14 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     // every XOR result out of the loop into a register of its own.
     asm volatile("" : "+v"(rb), "+v"(tb0), "+v"(tb1), "+v"(dw));
     const int i0 = it * S::BQ;
-    // Key block 0 has the smallest keys: if it sees none of the tile's
-    // queries (or lies past Sk), no block of the wave does.
+    // Key block 0 has the smallest keys: if it lies past Sk, no block of the
+    // wave has keys.  Causal: the wave skips tiles none of its keys see.  A
+    // general band runs such tiles through the masked path instead (P = 0):
+    // its two-sided test makes the register allocator spill heavily, and
+    // they are at most BKV / BQ tiles per workgroup.
     const bool active =
-        (!CAUSAL || band.any(i0, i0 + S::BQ - 1, kvb(0), kvb(KB - 1) + 31)) && kvb(0) < Sk;
+        (MODE != kMaskCausal || band.any(i0, i0 + S::BQ - 1, kvb(0), kvb(KB - 1) + 31)) &&
+        kvb(0) < Sk;
     if (active) {
       f32x16 s[KB], dp[KB];
 #pragma unroll
@@ -237,18 +252,18 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int kvw = kvb(kb);
-        const int my_kv = kvw + lr;
         const int wkv_last = min(kvw + 31, Sk - 1);
         const bool need_mask = (CAUSAL && !band.all(i0, i0 + S::BQ - 1, kvw, wkv_last)) ||
                                (kvw + 32 > Sk) || (i0 + S::BQ > Sq);
         // P = exp2(S·scale·log2e − lse2), dS = P (dP − rowdot).  Element
-        // (g, r) is query i0 + 8g + 4lh + r; on masked tiles it sees key
-        // my_kv iff c = 8g + r lies in [t_lo, t_hi); masked elements get
-        // P = 0.  The masked and unmasked forms are separate code paths so
-        // that the uniform branch between them stays a branch.
+        // (g, r) is query i0 + 8g + 4lh + r; on masked tiles it sees the
+        // lane's key iff c = 8g + r lies in [t_lo, t_hi); masked elements
+        // get P = 0.  The masked and unmasked forms are separate code paths
+        // so that the uniform branch between them stays a branch.
         auto softmax = [&](auto masked) {
           constexpr bool kMasked = decltype(masked)::value;
           const int rel = i0 + 4 * lh;
+          const int my_kv = kvw + lr;
           // j <= i + off + wr  <=>  c >= j - off - wr - rel;
           // j >= i + off - wl  <=>  c <= j - off + wl - rel.
           const int t_lo = (CAUSAL && band.wr >= 0) ? my_kv - off - band.wr - rel : -0x40000000;
@@ -320,16 +335,18 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     }
   };
 
-  // dQ[i0 + q][32w + d] += sum over the workgroup's keys of dS K, for the
-  // tile whose dSᵀ is complete in dsb (waves 0 .. DQW-1, one d tile each).
+  // dQ[i0 + q][32 dt + d] += sum over the workgroup's keys of dS K, for the
+  // tile whose dSᵀ is complete in dsb (waves 0 .. DQW-1, d tiles
+  // dt = wave + DQW j).
   auto dq_step = [&](int h_rel, int it, const char* dsb) {
     const int i0 = it * S::BQ;
     const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
     if (wave < S::DQW && any) {
-      const int dt = wave;
-      f32x16 acc;
+      f32x16 acc[S::DTW];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+      for (int j = 0; j < S::DTW; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[j][i] = 0.f;
 #pragma unroll
       for (int kc = 0; kc < S::BKV / 16; ++kc) {
         const int par = 4 * (kc & 1);
@@ -337,26 +354,34 @@ void bwd_main_d128_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
                                        8 * (ds_p ^ ((ds_r >> 2) + par)));
         const u32x2 s_hi = lds_read_tr(dsb + (16 * kc + ds_r + 8) * S::DS_ROWB +
                                        8 * (ds_p ^ (((ds_r + 8) >> 2) + par)));
-        const int ro = kc * 16 * S::ROWB;
-        const u32x2 k_lo = lds_read_tr(Ks + toff(0, dt) + ro);
-        const u32x2 k_hi = lds_read_tr(Ks + toff(1, dt) + ro);
         const u32x4 as = {s_lo[0], s_lo[1], s_hi[0], s_hi[1]};
-        const u32x4 bk = {k_lo[0], k_lo[1], k_hi[0], k_hi[1]};
-        acc = T::mma32(as, bk, acc);
+        const int ro = kc * 16 * S::ROWB;
+#pragma unroll
+        for (int j = 0; j < S::DTW; ++j) {
+          const int dt = wave + S::DQW * j;
+          const u32x2 k_lo = lds_read_tr(Ks + toff(0, dt) + ro);
+          const u32x2 k_hi = lds_read_tr(Ks + toff(1, dt) + ro);
+          const u32x4 bk = {k_lo[0], k_lo[1], k_hi[0], k_hi[1]};
+          acc[j] = T::mma32(as, bk, acc[j]);
+        }
       }
-      sched_pipeline<S::BKV / 16, 4, 1, 3>();
-      // acc[4g + r] = dQ[query i0 + 8g + 4lh + r][d 32dt + lr]; dqacc is
+      sched_pipeline<S::BKV / 16, 2 + 2 * S::DTW, S::DTW, 3>();
+      // acc[j][4g + r] = dQ[query i0 + 8g + 4lh + r][d 32dt + lr]; dqacc is
       // [B, H, Sq, D].  The resource ends after column 31 of the tile's last
       // valid row, so atomics for rows at or past Sq are dropped.
-      const float* dqh = dqacc + ((head_rows + h_rel) * Sq + i0) * D + 32 * dt;
       const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
-      const rsrc_t rd = make_rsrc(dqh, ((nrows - 1) * D + 32) * 4u);
       const uint32_t lo = 4u * (4 * lh * D + lr);
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+      for (int j = 0; j < S::DTW; ++j) {
+        const int dt = wave + S::DQW * j;
+        const float* dqh = dqacc + ((head_rows + h_rel) * Sq + i0) * D + 32 * dt;
+        const rsrc_t rd = make_rsrc(dqh, ((nrows - 1) * D + 32) * 4u);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          buffer_atomic_add(rd, lo, 4u * (8 * g + r) * D, acc[4 * g + r]);
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            buffer_atomic_add(rd, lo, 4u * (8 * g + r) * D, acc[j][4 * g + r]);
+      }
     }
   };
 

@@ -117,8 +117,8 @@ static int check_bwd(const fa_bwd_args* a) {
     return fail(FA_E_INVALID, "fa_bwd: null tensor pointer");
   if (a->dtype != FA_DTYPE_F16 && a->dtype != FA_DTYPE_BF16)
     return fail(FA_E_UNSUPPORTED, "fa_bwd: dtype %d not supported", a->dtype);
-  if (a->head_dim != 64 && a->head_dim != 128)
-    return fail(FA_E_UNSUPPORTED, "fa_bwd: head_dim %d not in {64,128}", a->head_dim);
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+    return fail(FA_E_UNSUPPORTED, "fa_bwd: head_dim %d not in {64,128,256}", a->head_dim);
   if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_k < 0)
     return fail(FA_E_INVALID, "fa_bwd: negative size");
   if (a->num_heads <= 0 || a->num_heads_k <= 0 || a->num_heads % a->num_heads_k != 0)

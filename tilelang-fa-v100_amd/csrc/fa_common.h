@@ -172,6 +172,26 @@ __device__ __host__ __forceinline__ Band make_band(const Args& a) {
   return Band{a.seqlen_k - a.seqlen_q, wl, wr};
 }
 
+// Mask variants a kernel is instantiated for.  kMaskCausal is the band
+// wl = -1, wr = 0 and kMaskNone wl = wr = -1; building them from constants
+// lets the compiler fold the window tests away (they cost registers in the
+// hot loops).
+enum MaskMode { kMaskNone = 0, kMaskCausal = 1, kMaskBand = 2 };
+
+template <class Args>
+__host__ __forceinline__ int mask_mode(const Args& a) {
+  const Band b = make_band(a);
+  if (b.wl < 0 && b.wr < 0) return kMaskNone;
+  return (b.wl < 0 && b.wr == 0) ? kMaskCausal : kMaskBand;
+}
+
+template <int MODE, class Args>
+__device__ __forceinline__ Band mode_band(const Args& a) {
+  if constexpr (MODE == kMaskCausal) return Band{a.seqlen_k - a.seqlen_q, -1, 0};
+  if constexpr (MODE == kMaskNone) return Band{a.seqlen_k - a.seqlen_q, -1, -1};
+  return make_band(a);
+}
+
 // Instruction-scheduling hint for a loop of N steps that each issue L LDS
 // reads followed by M matrix products: the reads of the first `ahead` steps
 // go first, then every step's products are followed by the reads of step

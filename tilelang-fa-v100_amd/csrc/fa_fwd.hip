@@ -69,9 +69,9 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
   }
 }
 
-// BANDED: causal or windowed (row key ranges move with the row); used for
-// the tile order only, the masks come from the arguments.
-template <class T, int D, bool BANDED>
+// MODE (MaskMode): full attention, causal, or a window band from the
+// arguments.  The causal and full bands are compile-time constants.
+template <class T, int D, int MODE>
 __global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
 void fwd_dense_kernel(fa_fwd_args a) {
   using C = FwdKernelCfg<D>;
@@ -81,7 +81,7 @@ void fwd_dense_kernel(fa_fwd_args a) {
   const int h = bh % a.num_heads;
   const int b = bh / a.num_heads;
   // Heaviest causal tiles (largest query index) first.
-  const int qt = BANDED ? qtiles - 1 - th.rank : th.rank;
+  const int qt = MODE != kMaskNone ? qtiles - 1 - th.rank : th.rank;
   const int hk = h / (a.num_heads / a.num_heads_k);
 
   DenseRows P;
@@ -97,7 +97,7 @@ void fwd_dense_kernel(fa_fwd_args a) {
   P.nrows = a.seqlen_q;
   P.sk = a.seqlen_k;
   P.off = a.seqlen_k - a.seqlen_q;
-  const Band band = make_band(a);
+  const Band band = mode_band<MODE>(a);
   P.wl = band.wl;
   P.wr = band.wr;
   P.has_lse = a.lse != nullptr;
@@ -260,11 +260,13 @@ static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   using C = FwdKernelCfg<D>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
-  const Band band = make_band(a);
-  if (band.wl >= 0 || band.wr >= 0)
-    hipLaunchKernelGGL((fwd_dense_kernel<T, D, true>), grid, dim3(C::THREADS), 0, st, a);
+  const int mode = mask_mode(a);
+  if (mode == kMaskCausal)
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskCausal>), grid, dim3(C::THREADS), 0, st, a);
+  else if (mode == kMaskBand)
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskBand>), grid, dim3(C::THREADS), 0, st, a);
   else
-    hipLaunchKernelGGL((fwd_dense_kernel<T, D, false>), grid, dim3(C::THREADS), 0, st, a);
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskNone>), grid, dim3(C::THREADS), 0, st, a);
   return hipGetLastError();
 }
 

@@ -95,9 +95,6 @@ def bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, determi
 def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
              deterministic: bool = False, window=(-1, -1)):
     """Returns (dq, dk, dv), each contiguous [B, S, H, D] in q's dtype."""
-    if q.shape[-1] not in (64, 128):
-        raise NotImplementedError(f"backward for head_dim {q.shape[-1]} is not implemented "
-                                  "(supported: 64, 128)")
     q, k, v, out, dout = (rows_ready(t) for t in (q, k, v, out, dout))
     if dout.dtype != q.dtype:
         dout = dout.to(q.dtype)
