@@ -71,11 +71,20 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   using S = BwdShapeMfma<D_, KB>;
   constexpr bool CAUSAL = MODE != kMaskNone;  // some (query, key) pairs are outside the band
   constexpr int D = S::D;
-  __shared__ __attribute__((aligned(16))) char Ks[S::K_BYTES];
-  __shared__ __attribute__((aligned(16))) char Q0[S::QT_BYTES], O0[S::QT_BYTES];
-  __shared__ __attribute__((aligned(16))) char Q1[S::QT_BYTES], O1[S::QT_BYTES];
-  __shared__ __attribute__((aligned(16))) float st0[2 * S::BQ], st1[2 * S::BQ];
-  __shared__ __attribute__((aligned(16))) char dS0[S::DS_BYTES], dS1[S::DS_BYTES];
+  // One LDS array.  The statistics and the Q / dO tiles come first, so
+  // their array offsets are instruction immediates (the 16-bit offset field
+  // reaches 64 KB); dSᵀ and K are addressed through per-lane bases that
+  // include their offsets.  Bases are combined with XOR constants below bit
+  // 9, so those offsets are multiples of 512.
+  constexpr int OFF_ST0 = 0, OFF_ST1 = 2 * S::BQ * 4;
+  constexpr int OFF_Q0 = 512, OFF_O0 = OFF_Q0 + S::QT_BYTES, OFF_Q1 = OFF_O0 + S::QT_BYTES,
+                OFF_O1 = OFF_Q1 + S::QT_BYTES;
+  constexpr int OFF_DS0 = OFF_O1 + S::QT_BYTES, OFF_DS1 = OFF_DS0 + S::DS_BYTES;
+  constexpr int OFF_K = OFF_DS1 + S::DS_BYTES;
+  static_assert(OFF_ST1 + 2 * S::BQ * 4 <= OFF_Q0 && OFF_K % 512 == 0 && OFF_DS0 % 512 == 0,
+                "LDS layout");
+  __shared__ __attribute__((aligned(16))) char smem[OFF_K + S::K_BYTES];
+  char* const Ks = smem + OFF_K;
 
   const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads, Hk = a.num_heads_k;
   const int G = H / Hk;
@@ -132,6 +141,9 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   // 16((2c + lh) ^ sw) = 32(c ^ (sw >> 1)) + 16(lh ^ (sw & 1)).
   int rb = lr * S::ROWB + 16 * (lh ^ (sw_lr & 1)) + 32 * (sw_lr >> 1);
   auto rm_off = [&](int c) { return rb ^ (32 * c); };
+  // The same for the wave's own K rows (array offset included).
+  int rbk = rb + OFF_K + wrow * S::ROWB;
+  auto rk_off = [&](int c) { return rbk ^ (32 * c); };
   // Transpose read of rows 16k + r (r = 4(lane/32) + (lane%16)/4, +8 for
   // hf = 1), columns 32dt + 16((lane/16)%2) + 4(lane%4) of a 256 B-row tile:
   // 16((4dt + q) ^ swz(r)) = 64(dt ^ (r & 3)) + 16(q ^ ((r >> 2) & 3)).
@@ -146,11 +158,18 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   // dSᵀ row wrow + 32kb + lr, piece 2g + lh: 8((2g + lh) ^ m) with
   // m = (row >> 2) & 7 = (lr >> 2) & 7 = 16(g ^ (m >> 1)) + 8(lh ^ (m & 1)).
   const int dsw_m = (lr >> 2) & 7;
-  int dw = (wrow + lr) * S::DS_ROWB + 16 * (dsw_m >> 1) + 8 * (lh ^ (dsw_m & 1));
+  int dw = OFF_DS0 + (wrow + lr) * S::DS_ROWB + 16 * (dsw_m >> 1) + 8 * (lh ^ (dsw_m & 1));
   auto dsw_off = [&](int kb, int g) { return (dw ^ (16 * g)) + 32 * kb * S::DS_ROWB; };
-  // dSᵀ transpose reads: rows 16kc + r, piece 4((k/16)%2) + k%4.
+  // dSᵀ transpose reads: rows 16kc + r (+8 for hf = 1), piece p =
+  // 4((k/16)%2) + k%4 stored at p ^ m, m = (row >> 2) & 7 = (r >> 2) +
+  // 4(kc & 1) + 2hf; all three terms occupy distinct bits, so the offset is
+  // a base XOR 32(kc & 1) XOR 16hf, plus (16kc + 8hf) rows as an immediate.
   const int ds_r = 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int ds_p = 4 * ((lane >> 4) & 1) + (lane & 3);
+  int dsr = OFF_DS0 + ds_r * S::DS_ROWB + 8 * (ds_p ^ (ds_r >> 2));
+  auto dsr_off = [&](int kc, int hf) {
+    return (dsr ^ (32 * (kc & 1)) ^ (16 * hf)) + (16 * kc + 8 * hf) * S::DS_ROWB;
+  };
 
   f32x16 dk[KB][D / 32], dv[KB][D / 32];
 #pragma unroll
@@ -171,7 +190,9 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   // Q / dO tile loader: 32 rows = QT_BLOCKS blocks of 1 KB; each wave loads
   // QT_BLOCKS / NW of them.  Lane l of block blk holds row RPB blk + l/CPR,
   // stored chunk l%CPR (logical chunk (l%CPR) ^ swz(row)); its byte offset
-  // from the tile's first row is fixed.
+  // from the tile's first row is fixed.  (Leaving the DMA to the waves
+  // without dQ work, so that the dQ waves never wait for their atomics at
+  // the barrier, measured slower.)
   constexpr int BPW = S::QT_BLOCKS / S::NW;
   uint32_t q_loff[BPW], o_loff[BPW];
 #pragma unroll
@@ -182,9 +203,9 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     o_loff[ii] = 2u * (r * (uint32_t)a.do_stride[1] + 8 * c);
   }
 
-  // Tile t covers query head hk*G + t / nit and query tile it0 + t % nit;
+  // Tile t covers query head hk*G + t / nit and query tile it1 - 1 - t % nit;
   // (h_rel, it) is carried incrementally so the loop has no integer division.
-  auto issue_q = [&](int h_rel, int it, char* qb, char* ob, float* st) {
+  auto issue_q = [&](int h_rel, int it, int qo, int oo, int so) {
     const int h = hk * G + h_rel;
     const int i0 = it * S::BQ;
     // Buffer resources over the tile's valid rows: rows at or past Sq read
@@ -194,30 +215,36 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     const uint16_t* orow = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
                            h * a.do_stride[2] + (int64_t)i0 * a.do_stride[1];
     const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
-    const rsrc_t rq = make_rsrc(qrow, nrows * (uint32_t)a.q_stride[1] * 2u);
-    const rsrc_t ro = make_rsrc(orow, nrows * (uint32_t)a.do_stride[1] * 2u);
+    const u32x4 rq = rsrc_words(qrow, nrows * (uint32_t)a.q_stride[1] * 2u);
+    const u32x4 ro = rsrc_words(orow, nrows * (uint32_t)a.do_stride[1] * 2u);
+    // Opaque DMA: the loop's wait_vmem + barrier is the only wait the tile
+    // needs (the compiler would otherwise wait for it, and for the dQ
+    // atomics, before each dSᵀ access).
 #pragma unroll
     for (int ii = 0; ii < BPW; ++ii) {
       const int blk = BPW * wave + ii;
-      buffer_lds16(rq, q_loff[ii], qb + blk * 1024);
-      buffer_lds16(ro, o_loff[ii], ob + blk * 1024);
+      buffer_lds16_opaque(rq, q_loff[ii], smem + qo + blk * 1024);
+      buffer_lds16_opaque(ro, o_loff[ii], smem + oo + blk * 1024);
     }
     if (wave == 0) {
       // Lanes 0-31 fetch LSE*log2(e), lanes 32-63 rowdot ([B*H][2][Sq]).
       const float* sbase = stats + 2 * (head_rows + h_rel) * Sq + i0;
       const unsigned lo = (lane >> 5) * Sq + min(lane & 31, Sq - 1 - i0);
-      __builtin_amdgcn_global_load_lds(sbase + lo, (__attribute__((address_space(3))) void*)st,
-                                       4, 0, 0);
+      global_lds4_opaque(sbase + lo, smem + so);
     }
   };
 
   // S, dP, softmax, dSᵀ -> dsb, dV and dK for one query tile (no barrier).
-  auto step = [&](int h_rel, int it, const char* qb, const char* ob, const float* st,
-                  char* dsb) {
+  // qo, oo, so: offsets of the Q, dO and statistics tiles; dso: 0 for dSᵀ
+  // buffer 0, DS_BYTES for buffer 1.
+  auto step = [&](int h_rel, int it, int qo, int oo, int so, int dso) {
+    const char* qb = smem + qo;
+    const char* ob = smem + oo;
+    const float* st = reinterpret_cast<const float*>(smem + so);
     // The per-chunk offsets are `base ^ constant`.  Marking the bases as
     // (opaquely) rewritten each iteration keeps the compiler from hoisting
     // every XOR result out of the loop into a register of its own.
-    asm volatile("" : "+v"(rb), "+v"(tb0), "+v"(tb1), "+v"(dw));
+    asm volatile("" : "+v"(rb), "+v"(tb0), "+v"(tb1), "+v"(dw), "+v"(rbk));
     const int i0 = it * S::BQ;
     // Key block 0 has the smallest keys: if it lies past Sk, no block of the
     // wave has keys.  Causal: the wave skips tiles none of its keys see.  A
@@ -239,7 +266,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
         const u32x4 ao = ld16(ob + rm_off(c));
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          const u32x4 bk = ld16(Ks + (wrow + 32 * kb) * S::ROWB + rm_off(c));
+          const u32x4 bk = ld16(smem + rk_off(c) + 32 * kb * S::ROWB);
           s[kb] = T::mma32(aq, bk, s[kb]);
           dp[kb] = T::mma32(ao, vB[kb][c], dp[kb]);
         }
@@ -304,7 +331,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
         for (int g = 0; g < 4; ++g) {
           const int kq = g >> 1, w0 = 2 * (g & 1);
           const u32x2 v = {sB[kb][kq][w0], sB[kb][kq][w0 + 1]};
-          st8(dsb + dsw_off(kb, g), v);
+          st8(smem + dso + dsw_off(kb, g), v);
         }
       }
       // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads, shared
@@ -331,41 +358,48 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) st8(dsb + dsw_off(kb, g), u32x2{0, 0});
+        for (int g = 0; g < 4; ++g) st8(smem + dso + dsw_off(kb, g), u32x2{0, 0});
     }
   };
 
   // dQ[i0 + q][32 dt + d] += sum over the workgroup's keys of dS K, for the
   // tile whose dSᵀ is complete in dsb (waves 0 .. DQW-1, d tiles
   // dt = wave + DQW j).
-  auto dq_step = [&](int h_rel, int it, const char* dsb) {
+  auto dq_step = [&](int h_rel, int it, int dso) {
     const int i0 = it * S::BQ;
     const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
     if (wave < S::DQW && any) {
+      asm volatile("" : "+v"(dsr));
       f32x16 acc[S::DTW];
 #pragma unroll
       for (int j = 0; j < S::DTW; ++j)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[j][i] = 0.f;
+      struct DqOps {
+        u32x2 s_lo, s_hi, k_lo[S::DTW], k_hi[S::DTW];
+      };
+      lds_pipeline<S::BKV / 16, 2>(
+          [&](int kc) {
+            DqOps o;
+            o.s_lo = lds_read_tr(smem + dso + dsr_off(kc, 0));
+            o.s_hi = lds_read_tr(smem + dso + dsr_off(kc, 1));
+            const int ro = kc * 16 * S::ROWB;
 #pragma unroll
-      for (int kc = 0; kc < S::BKV / 16; ++kc) {
-        const int par = 4 * (kc & 1);
-        const u32x2 s_lo = lds_read_tr(dsb + (16 * kc + ds_r) * S::DS_ROWB +
-                                       8 * (ds_p ^ ((ds_r >> 2) + par)));
-        const u32x2 s_hi = lds_read_tr(dsb + (16 * kc + ds_r + 8) * S::DS_ROWB +
-                                       8 * (ds_p ^ (((ds_r + 8) >> 2) + par)));
-        const u32x4 as = {s_lo[0], s_lo[1], s_hi[0], s_hi[1]};
-        const int ro = kc * 16 * S::ROWB;
+            for (int j = 0; j < S::DTW; ++j) {
+              const int dt = wave + S::DQW * j;
+              o.k_lo[j] = lds_read_tr(Ks + toff(0, dt) + ro);
+              o.k_hi[j] = lds_read_tr(Ks + toff(1, dt) + ro);
+            }
+            return o;
+          },
+          [&](int, const DqOps& o) {
+            const u32x4 as = {o.s_lo[0], o.s_lo[1], o.s_hi[0], o.s_hi[1]};
 #pragma unroll
-        for (int j = 0; j < S::DTW; ++j) {
-          const int dt = wave + S::DQW * j;
-          const u32x2 k_lo = lds_read_tr(Ks + toff(0, dt) + ro);
-          const u32x2 k_hi = lds_read_tr(Ks + toff(1, dt) + ro);
-          const u32x4 bk = {k_lo[0], k_lo[1], k_hi[0], k_hi[1]};
-          acc[j] = T::mma32(as, bk, acc[j]);
-        }
-      }
-      sched_pipeline<S::BKV / 16, 2 + 2 * S::DTW, S::DTW, 3>();
+            for (int j = 0; j < S::DTW; ++j) {
+              const u32x4 bk = {o.k_lo[j][0], o.k_lo[j][1], o.k_hi[j][0], o.k_hi[j][1]};
+              acc[j] = T::mma32(as, bk, acc[j]);
+            }
+          });
       // acc[j][4g + r] = dQ[query i0 + 8g + 4lh + r][d 32dt + lr]; dqacc is
       // [B, H, Sq, D].  The resource ends after column 31 of the tile's last
       // valid row, so atomics for rows at or past Sq are dropped.
@@ -385,11 +419,15 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     }
   };
 
-  int ih = 0, ii = it0;  // tile to issue next
-  int ch = 0, ci = it0;  // tile to compute next
+  // Query tiles are swept from the last down: the workgroups of one head
+  // that run at the same time (consecutive key tiles) then add into the
+  // same dQ rows at about the same time, which keeps those rows in L2 for
+  // the atomics (measured ~3% faster than the ascending sweep).
+  int ih = 0, ii = it1 - 1;  // tile to issue next
+  int ch = 0, ci = it1 - 1;  // tile to compute next
   auto advance = [&](int& h_rel, int& it) {
-    if (++it == it1) {
-      it = it0;
+    if (it-- == it0) {
+      it = it1 - 1;
       ++h_rel;
     }
   };
@@ -399,19 +437,19 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   // products.  dSᵀ alternates between dS0 and dS1.
   int ph = 0, pi = 0;  // tile whose dQ is pending
   if (ntot > 0) {
-    issue_q(ih, ii, Q0, O0, st0);
+    issue_q(ih, ii, OFF_Q0, OFF_O0, OFF_ST0);
     advance(ih, ii);
   }
   for (int t = 0; t < ntot; t += 2) {
     wait_vmem();
     __syncthreads();
     if (t + 1 < ntot) {
-      issue_q(ih, ii, Q1, O1, st1);
+      issue_q(ih, ii, OFF_Q1, OFF_O1, OFF_ST1);
       advance(ih, ii);
     }
-    if (t > 0) dq_step(ph, pi, dS1);
+    if (t > 0) dq_step(ph, pi, S::DS_BYTES);
     __builtin_amdgcn_sched_barrier(0);  // keep the two phases' registers apart
-    step(ch, ci, Q0, O0, st0, dS0);
+    step(ch, ci, OFF_Q0, OFF_O0, OFF_ST0, 0);
     ph = ch;
     pi = ci;
     advance(ch, ci);
@@ -419,12 +457,12 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
       wait_vmem();
       __syncthreads();
       if (t + 2 < ntot) {
-        issue_q(ih, ii, Q0, O0, st0);
+        issue_q(ih, ii, OFF_Q0, OFF_O0, OFF_ST0);
         advance(ih, ii);
       }
-      dq_step(ph, pi, dS0);
+      dq_step(ph, pi, 0);
       __builtin_amdgcn_sched_barrier(0);
-      step(ch, ci, Q1, O1, st1, dS1);
+      step(ch, ci, OFF_Q1, OFF_O1, OFF_ST1, S::DS_BYTES);
       ph = ch;
       pi = ci;
       advance(ch, ci);
@@ -432,7 +470,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   }
   if (ntot > 0) {
     __syncthreads();  // dSᵀ of the last tile complete
-    dq_step(ph, pi, ((ntot - 1) & 1) ? dS1 : dS0);
+    dq_step(ph, pi, ((ntot - 1) & 1) ? S::DS_BYTES : 0);
   }
   wait_vmem();
 

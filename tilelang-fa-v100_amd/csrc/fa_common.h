@@ -207,6 +207,27 @@ __device__ __forceinline__ void sched_pipeline() {
   }
 }
 
+// Software pipeline of N steps whose operands come from LDS: the reads of
+// step k + AHEAD are issued before the products of step k, with a
+// scheduling barrier after every step, so AHEAD + 1 operand sets are live
+// and each product waits only for its own reads (lgkmcnt of the later
+// steps' reads).  load(k) returns step k's operands; use(k, ops) consumes
+// them.  (The compiler's own scheduler, under register pressure, falls
+// back to issuing each step's reads right before its products.)
+template <int N, int AHEAD, class Load, class Use>
+__device__ __forceinline__ void lds_pipeline(Load load, Use use) {
+  using Ops = decltype(load(0));
+  Ops ring[AHEAD + 1];
+#pragma unroll
+  for (int k = 0; k < AHEAD && k < N; ++k) ring[k] = load(k);
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    if (k + AHEAD < N) ring[(k + AHEAD) % (AHEAD + 1)] = load(k + AHEAD);
+    use(k, ring[k % (AHEAD + 1)]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Buffer resources (gfx9 format): a 128-bit descriptor in scalar registers
 // plus a 32-bit per-lane byte offset.  Accesses at offsets >= `bytes` are
 // dropped (stores, atomics) or return zero (loads), which the kernels use to
@@ -226,6 +247,40 @@ __device__ __forceinline__ void buffer_lds16(rsrc_t r, uint32_t voff, char* lds_
 __device__ __forceinline__ void buffer_lds4(rsrc_t r, uint32_t voff, void* lds_block) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       r, (__attribute__((address_space(3))) void*)lds_block, 4, voff, 0, 0, 0);
+}
+// Buffer descriptor words for the inline-assembly DMA below (same fields as
+// make_rsrc: raw buffer, stride 0, num_records = bytes).
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xFFFFu, bytes, (uint32_t)kRsrcFlags};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// LDS DMA the compiler does not see: buffer_lds16 / a 4-byte global_load_lds
+// issued from inline assembly.  The compiler treats every LDS access after a
+// DMA it knows of as possibly aliasing the DMA target unless it can prove
+// otherwise, and then waits for vmcnt(0) - which also waits for every
+// outstanding global atomic.  With these forms the caller owns the wait:
+// wait_vmem() before any wave reads the target (followed by a barrier when
+// other waves read it).
+__device__ __forceinline__ void buffer_lds16_opaque(u32x4 rsrc, uint32_t voff, char* lds_block) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(lds_addr(lds_block))
+      : "memory", "m0");
+}
+__device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_block) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %0, off"
+      :
+      : "v"(src), "s"(lds_addr(lds_block))
+      : "memory", "m0");
 }
 // Atomic fp32 add at base + voff + soff (no return value).
 __device__ __forceinline__ void buffer_atomic_add(rsrc_t r, uint32_t voff, uint32_t soff,
