@@ -56,7 +56,8 @@ typedef enum fa_dtype {
 
 /* ------------------------------------------------------------------------ */
 /* Dense attention, FA2 layout q/k/v/out [batch, seqlen, heads, head_dim].   */
-/* Strides are in elements: {batch, seq, head}; head_dim is contiguous.     */
+/* Strides are in elements: {batch, seq, head}; head_dim is contiguous;    */
+/* k / v sequence strides below 2^24 elements.                             */
 /* Causal masking is bottom-right aligned: key j is visible to query i iff  */
 /* j <= i + seqlen_k - seqlen_q (tests/test_compare_ref.py:22 convention).  */
 /* Sliding window (FlashAttention-2 window_size, off = seqlen_k - seqlen_q),*/

@@ -103,6 +103,14 @@ def test_fwd_rejects_unaligned_stride():
     assert _lib.load().fa_fwd(ctypes.byref(a), None) == _lib.FA_E_UNSUPPORTED
 
 
+@pytest.mark.parametrize("name", ["k_stride", "v_stride"])
+def test_fwd_rejects_kv_sequence_stride_beyond_2_pow_24(name):
+    a = fwd_args()
+    getattr(a, name)[1] = 1 << 24
+    assert _lib.load().fa_fwd(ctypes.byref(a), None) == _lib.FA_E_UNSUPPORTED
+    assert b"2^24" in _lib.load().fa_last_error_message()
+
+
 def bwd_args(**over):
     a = _lib.BwdArgs()
     for n in ("q", "k", "v", "out", "dout", "lse", "dq", "dk", "dv"):

@@ -53,6 +53,7 @@ constexpr int64_t kIntMax = 0x7fffffff;
 // Kernels address up to 32 rows past a uniform row base with unsigned 32-bit
 // offsets, so per-row (sequence) strides must stay below 2^26 elements.
 constexpr int64_t kMaxRowStride = int64_t(1) << 26;
+constexpr int64_t kMaxFwdKvRowStride = int64_t(1) << 24;
 
 }  // namespace
 
@@ -95,6 +96,10 @@ static int check_fwd(const fa_fwd_args* a) {
     return fail(FA_E_UNSUPPORTED, "fa_fwd: strides must be non-negative multiples of 8");
   if (a->has_window && (a->window_left < -1 || a->window_right < -1))
     return fail(FA_E_INVALID, "fa_fwd: window sizes must be >= -1");
+  // The head_dim 128 core DMAs K / V tiles through buffer resources with
+  // 32-bit lane offsets of up to 64 rows.
+  if (a->k_stride[1] >= kMaxFwdKvRowStride || a->v_stride[1] >= kMaxFwdKvRowStride)
+    return fail(FA_E_UNSUPPORTED, "fa_fwd: k / v sequence strides must be below 2^24 elements");
   const int64_t tiles = ((int64_t)a->seqlen_q + 127) / 128 * a->num_heads * a->batch;
   if (tiles > kIntMax) return fail(FA_E_UNSUPPORTED, "fa_fwd: problem too large");
   return ok();

@@ -26,6 +26,9 @@ struct DenseRows {
   int nrows, sk, off;      // off = seqlen_k - seqlen_q
   int wl, wr;              // window bounds (-1: unbounded); causal is wr = 0
   bool has_lse;
+  // K / V rows are a base plus a row stride (below 2^24 elements, checked
+  // by the launcher), so whole tiles can be DMA'd through buffer resources.
+  static constexpr bool kRowStrided = true;
 
   // Row r sees keys [r + off - wl, r + off + wr] within [0, sk).
   __device__ int kv_lo(int r) const { return wl >= 0 ? min(max(r + off - wl, 0), sk) : 0; }
@@ -116,6 +119,7 @@ struct PagedRows {
   int ps_log2, ps_mask, last_page;
   int G, nrows, seq_len, prefix, wq, wk;
   bool causal, has_lse;
+  static constexpr bool kRowStrided = false;
 
   __device__ int kv_lo(int r) const {
     if (!causal || wq <= 0) return 0;

@@ -124,37 +124,46 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   float ms_run = neg_inf();
   float l_run = 0.f;
 
-  // ---- tile loader: wave w fills 1 KB blocks 2w, 2w+1 (rows 8w .. 8w+7) of
-  // the K and V tiles.  Lane l of block b holds row 4b + l/16, stored chunk
+  // ---- tile loaders: wave w fills 1 KB blocks 2w, 2w+1 (rows 8w .. 8w+7)
+  // of a K or V tile.  Lane l of block b holds row 4b + l/16, stored chunk
   // l%16, i.e. logical chunk (l%16) ^ swz(row).
   const int ld_last = max(wg_hi - 1, 0);
-  auto issue_tile = [&](int n0, char* kb, char* vb) {
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const int blk = 2 * wave + ii;
-      const int r = 4 * blk + (lane >> 4);
-      const int c = (lane & 15) ^ swz_chunk(r);
-      const int n = min(n0 + r, ld_last);
-      load_lds16(P.k_ptr(n) + 8 * c, kb + blk * 1024);
-      load_lds16(P.v_ptr(n) + 8 * c, vb + blk * 1024);
-    }
-  };
-
-  auto compute_tile = [&](int n0, const char* kb, const char* vb) {
-    if (!(wave_active && n0 < w_hi_max && n0 + BN > w_lo_min)) return;
-    f32x16 s[BN / 32];
+  // Tile n0 has keys this wave's rows see.
+  auto visible = [&](int n0) { return wave_active && n0 < w_hi_max && n0 + BN > w_lo_min; };
+  f32x16 s[BN / 32];
+  u32x4 pb[BN / 16];
+  // Operand reads run kAheadS / kAheadO steps ahead of the products.
+#ifndef FA_FWD_AHEAD_S
+#define FA_FWD_AHEAD_S 3
+#endif
+#ifndef FA_FWD_AHEAD_O
+#define FA_FWD_AHEAD_O 4
+#endif
+  constexpr int kAheadS = FA_FWD_AHEAD_S, kAheadO = FA_FWD_AHEAD_O;
+  // Sᵀ = K Qᵀ for tile n0 (keys from kb).  The key blocks' accumulation
+  // chains alternate (consecutive products are independent).
+  auto gemm_s = [&](const char* kb) {
 #pragma unroll
     for (int kt = 0; kt < BN / 32; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
-    // The key blocks' accumulation chains alternate (consecutive products are
-    // independent) and K reads run two chunks ahead of the products.
+    struct KOps {
+      u32x4 k[BN / 32];
+    };
+    lds_pipeline<D / 16, kAheadS>(
+        [&](int c) {
+          KOps r;
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c)
+          for (int kt = 0; kt < BN / 32; ++kt) r.k[kt] = ld16(kb + koff[c] + kt * 32 * S::ROWB);
+          return r;
+        },
+        [&](int c, const KOps& r) {
 #pragma unroll
-      for (int kt = 0; kt < BN / 32; ++kt)
-        s[kt] = T::mma32(ld16(kb + koff[c] + kt * 32 * S::ROWB), qf[c], s[kt]);
-    sched_pipeline<D / 16, BN / 32, BN / 32, 2>();
+          for (int kt = 0; kt < BN / 32; ++kt) s[kt] = T::mma32(r.k[kt], qf[c], s[kt]);
+        });
+  };
+  // Online softmax of s (tile n0) into the B operand pb of Oᵀ += Vᵀ Pᵀ.
+  auto softmax = [&](int n0) {
     const bool need_mask = (n0 < w_lo_max) || (n0 + BN > w_hi_min);
     if (need_mask) {
 #pragma unroll
@@ -183,7 +192,6 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
         for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
     }
     const float mb = ms_run == neg_inf() ? 0.f : ms_run;
-    u32x4 pb[BN / 16];
 #pragma unroll
     for (int kc = 0; kc < BN / 16; ++kc)
 #pragma unroll
@@ -194,33 +202,126 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
         pb[kc][w] = T::pack(p0, p1);
         l_run = T::sum2(p0, p1, pb[kc][w], l_run);
       }
-#pragma unroll
-    for (int kc = 0; kc < BN / 16; ++kc)
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const u32x2 lo = lds_read_tr(vb + voff[0][dt] + kc * 16 * S::ROWB);
-        const u32x2 hi = lds_read_tr(vb + voff[1][dt] + kc * 16 * S::ROWB);
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        o[dt] = T::mma32(a, pb[kc], o[dt]);
-      }
+  };
+  // Oᵀ += Vᵀ Pᵀ (V from vb).
+  auto gemm_o = [&](const char* vb) {
+    struct VOps {
+      u32x2 lo, hi;
+    };
+    lds_pipeline<(BN / 16) * (D / 32), kAheadO>(
+        [&](int k) {
+          const int kc = k / (D / 32), dt = k % (D / 32);
+          return VOps{lds_read_tr(vb + voff[0][dt] + kc * 16 * S::ROWB),
+                      lds_read_tr(vb + voff[1][dt] + kc * 16 * S::ROWB)};
+        },
+        [&](int k, const VOps& r) {
+          const int kc = k / (D / 32), dt = k % (D / 32);
+          const u32x4 a = {r.lo[0], r.lo[1], r.hi[0], r.hi[1]};
+          o[dt] = T::mma32(a, pb[kc], o[dt]);
+        });
   };
 
+  // Ping-pong schedule.  Waves 0-3 (group A) and 4-7 (group B) share the
+  // SIMDs pairwise; the loop runs in slots separated by workgroup barriers,
+  // and in every slot one wave of each SIMD runs matrix products (Oᵀ of the
+  // previous tile, then Sᵀ of the current one: 32 MFMAs) while the other
+  // runs the softmax (exp2, max, sums: VALU), so the two overlap instead of
+  // both waves reaching the same phase together.  Group B runs one slot
+  // behind group A:
+  //   slot 2j   A: O(j-1), S(j)   B: softmax(j-1)   DMA: K(j+1), V(j)
+  //   slot 2j+1 A: softmax(j)     B: O(j-1), S(j)   then wait for the DMA
+  // K(j) is read in slots 2j, 2j+1 and V(j) in 2j+2, 2j+3, so two buffers
+  // of each suffice: K(j+1) and V(j) overwrite K(j-1) and V(j-2), whose
+  // last reads were in slot 2j-1.  The loop body covers two tiles so that
+  // every buffer is a compile-time array (see the note on k0..v1 above).
+  const bool grp_b = wave >= S::NW / 2;
   const int j0 = max(wg_lo, 0) / BN;
   const int j1 = (wg_hi + BN - 1) / BN;
-  if (j0 < j1) issue_tile(j0 * BN, k0, v0);
-  for (int j = j0; j < j1; j += 2) {
-    // tile j in (k0, v0)
-    wait_vmem();
-    __syncthreads();  // tile j resident; everyone is done with tile j-1
-    if (j + 1 < j1) issue_tile((j + 1) * BN, k1, v1);
-    compute_tile(j * BN, k0, v0);
-    if (j + 1 >= j1) break;
-    // tile j+1 in (k1, v1)
-    wait_vmem();
-    __syncthreads();
-    if (j + 2 < j1) issue_tile((j + 2) * BN, k0, v0);
-    compute_tile((j + 1) * BN, k1, v1);
+  // Row-strided problems (dense) DMA through buffer resources: the lane's
+  // byte offset within the tile is fixed, the tile base is scalar, and rows
+  // at or past the last key read as zero (their scores are masked).  Paged
+  // problems resolve each row's page.
+  constexpr bool kStrided = Prob::kRowStrided;
+  uint32_t ld_off[2] = {0, 0};
+  if constexpr (kStrided) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int r = 4 * (2 * wave + ii) + (lane >> 4);
+      ld_off[ii] = 2u * ((uint32_t)r * (uint32_t)P.ks + 8u * ((lane & 15) ^ swz_chunk(r)));
+    }
   }
+  auto issue_rows = [&](int n0, char* dst, auto is_v) {
+    constexpr bool kV = decltype(is_v)::value;
+    if constexpr (kStrided) {
+      const uint16_t* base = kV ? P.v + (int64_t)n0 * P.vs : P.k + (int64_t)n0 * P.ks;
+      const uint32_t bytes = (uint32_t)min(BN, wg_hi - n0) * (uint32_t)(kV ? P.vs : P.ks) * 2u;
+      const u32x4 rs = rsrc_words(base, bytes);
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) buffer_lds16_opaque(rs, ld_off[ii], dst + (2 * wave + ii) * 1024);
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int blk = 2 * wave + ii;
+        const int r = 4 * blk + (lane >> 4);
+        const int c = (lane & 15) ^ swz_chunk(r);
+        const int n = min(n0 + r, ld_last);
+        load_lds16((kV ? P.v_ptr(n) : P.k_ptr(n)) + 8 * c, dst + blk * 1024);
+      }
+    }
+  };
+  auto issue_k = [&](int n0, char* kb) { issue_rows(n0, kb, BoolC<false>{}); };
+  auto issue_v = [&](int n0, char* vb) { issue_rows(n0, vb, BoolC<true>{}); };
+  // One slot: the matrix phase for tile j (O of j-1 from vprev, S of j from
+  // kcur) or the softmax phase for tile js.
+  auto mma_phase = [&](int j, const char* vprev, const char* kcur) {
+    if (j - 1 >= j0 && visible((j - 1) * BN)) gemm_o(vprev);
+    if (j < j1 && visible(j * BN)) gemm_s(kcur);
+  };
+  auto sm_phase = [&](int js) {
+    if (js >= j0 && js < j1 && visible(js * BN)) softmax(js * BN);
+  };
+  auto slot_barrier = [&](bool wait_dma) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (wait_dma) {
+      wait_vmem();
+      __syncthreads();
+    } else {
+      __builtin_amdgcn_s_barrier();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if (j0 < j1) issue_k(j0 * BN, k0);
+  wait_vmem();
+  __syncthreads();
+  // Each group runs its own copy of the loop (the barriers pair up across
+  // the copies: both execute the same number), so that in each copy only
+  // one of s / pb is live at a slot boundary.
+  auto run = [&](auto group_b) {
+    constexpr bool kB = decltype(group_b)::value;
+    for (int j = j0;; j += 2) {
+      // tile j: K in k0, V in v0; tile j-1: V in v1; tile j+1: K in k1.
+      if (j + 1 < j1) issue_k((j + 1) * BN, k1);
+      if (j < j1) issue_v(j * BN, v0);
+      if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0);
+      slot_barrier(false);
+      if (kB) mma_phase(j, v1, k0); else sm_phase(j);
+      slot_barrier(true);
+      if (j + 1 > j1) break;
+      // tile j+1: K in k1, V in v1; tile j: V in v0; tile j+2: K in k0.
+      if (j + 2 < j1) issue_k((j + 2) * BN, k0);
+      if (j + 1 < j1) issue_v((j + 1) * BN, v1);
+      if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1);
+      slot_barrier(false);
+      if (kB) mma_phase(j + 1, v0, k1); else sm_phase(j + 1);
+      slot_barrier(true);
+      if (j + 2 > j1) break;
+    }
+  };
+  if (grp_b)
+    run(BoolC<true>{});
+  else
+    run(BoolC<false>{});
 
   const float l_all = l_run + swap_halves(l_run);
   if (!row_valid) return;

@@ -50,6 +50,9 @@ def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1)):
     """Returns (out [B,Sq,H,D], lse [B,H,Sq] fp32)."""
     B, Sq, Sk, H, Hk, D = check_shapes(q, k, v)
     q, k, v = rows_ready(q), rows_ready(k), rows_ready(v)
+    # K / V sequence strides must stay below 2^24 elements (fa_fwd).
+    k = k.contiguous() if k.stride(1) >= 1 << 24 else k
+    v = v.contiguous() if v.stride(1) >= 1 << 24 else v
     out = torch.empty((B, Sq, H, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
     a = _lib.FwdArgs()
