@@ -228,7 +228,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   // runs the softmax (exp2, max, sums: VALU), so the two overlap instead of
   // both waves reaching the same phase together.  Group B runs one slot
   // behind group A:
-  //   slot 2j   A: O(j-1), S(j)   B: softmax(j-1)   DMA: K(j+1), V(j)
+  //   slot 2j   A: O(j-1), S(j), DMA K(j+1), V(j)   B: softmax(j-1)
   //   slot 2j+1 A: softmax(j)     B: O(j-1), S(j)   then wait for the DMA
   // K(j) is read in slots 2j, 2j+1 and V(j) in 2j+2, 2j+3, so two buffers
   // of each suffice: K(j+1) and V(j) overwrite K(j-1) and V(j-2), whose
@@ -237,16 +237,22 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   const bool grp_b = wave >= S::NW / 2;
   const int j0 = max(wg_lo, 0) / BN;
   const int j1 = (wg_hi + BN - 1) / BN;
-  // Row-strided problems (dense) DMA through buffer resources: the lane's
-  // byte offset within the tile is fixed, the tile base is scalar, and rows
-  // at or past the last key read as zero (their scores are masked).  Paged
-  // problems resolve each row's page.
+  // K / V tiles are DMA'd by group A alone, from inside its matrix phase:
+  // issuing 32 KB per tile from all eight waves at the start of a slot
+  // stalled them on the vector-memory queue; behind a burst of MFMAs the
+  // queueing overlaps the matrix core's work.  Wave w < 4 fills 1 KB blocks
+  // 4w .. 4w+3 (rows 16w .. 16w+15).  Row-strided problems (dense) DMA
+  // through buffer resources: the lane's byte offset within the tile is
+  // fixed, the tile base is scalar, and rows at or past the last key read
+  // as zero (their scores are masked).  Paged problems resolve each row's
+  // page.
+  constexpr int DB = 16 / (S::NW / 2);  // blocks per DMA wave and tile
   constexpr bool kStrided = Prob::kRowStrided;
-  uint32_t ld_off[2] = {0, 0};
+  uint32_t ld_off[DB] = {};
   if constexpr (kStrided) {
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const int r = 4 * (2 * wave + ii) + (lane >> 4);
+    for (int ii = 0; ii < DB; ++ii) {
+      const int r = 4 * (DB * wave + ii) + (lane >> 4);
       ld_off[ii] = 2u * ((uint32_t)r * (uint32_t)P.ks + 8u * ((lane & 15) ^ swz_chunk(r)));
     }
   }
@@ -257,11 +263,12 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
       const uint32_t bytes = (uint32_t)min(BN, wg_hi - n0) * (uint32_t)(kV ? P.vs : P.ks) * 2u;
       const u32x4 rs = rsrc_words(base, bytes);
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) buffer_lds16_opaque(rs, ld_off[ii], dst + (2 * wave + ii) * 1024);
+      for (int ii = 0; ii < DB; ++ii)
+        buffer_lds16_opaque(rs, ld_off[ii], dst + (DB * wave + ii) * 1024);
     } else {
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
-        const int blk = 2 * wave + ii;
+      for (int ii = 0; ii < DB; ++ii) {
+        const int blk = DB * wave + ii;
         const int r = 4 * blk + (lane >> 4);
         const int c = (lane & 15) ^ swz_chunk(r);
         const int n = min(n0 + r, ld_last);
@@ -272,10 +279,15 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   auto issue_k = [&](int n0, char* kb) { issue_rows(n0, kb, BoolC<false>{}); };
   auto issue_v = [&](int n0, char* vb) { issue_rows(n0, vb, BoolC<true>{}); };
   // One slot: the matrix phase for tile j (O of j-1 from vprev, S of j from
-  // kcur) or the softmax phase for tile js.
-  auto mma_phase = [&](int j, const char* vprev, const char* kcur) {
+  // kcur; group A also issues the DMA of K(j+1) into knext and V(j) into
+  // vcur) or the softmax phase for tile js.
+  auto mma_phase = [&](int j, const char* vprev, const char* kcur, char* knext, char* vcur,
+                       auto dma) {
+    constexpr bool kDma = decltype(dma)::value;
     if (j - 1 >= j0 && visible((j - 1) * BN)) gemm_o(vprev);
+    if (kDma && j + 1 < j1) issue_k((j + 1) * BN, knext);
     if (j < j1 && visible(j * BN)) gemm_s(kcur);
+    if (kDma && j < j1) issue_v(j * BN, vcur);
   };
   auto sm_phase = [&](int js) {
     if (js >= j0 && js < j1 && visible(js * BN)) softmax(js * BN);
@@ -291,7 +303,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (j0 < j1) issue_k(j0 * BN, k0);
+  if (j0 < j1 && !grp_b) issue_k(j0 * BN, k0);
   wait_vmem();
   __syncthreads();
   // Each group runs its own copy of the loop (the barriers pair up across
@@ -299,21 +311,18 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   // one of s / pb is live at a slot boundary.
   auto run = [&](auto group_b) {
     constexpr bool kB = decltype(group_b)::value;
+    constexpr BoolC<!kB> dma{};
     for (int j = j0;; j += 2) {
       // tile j: K in k0, V in v0; tile j-1: V in v1; tile j+1: K in k1.
-      if (j + 1 < j1) issue_k((j + 1) * BN, k1);
-      if (j < j1) issue_v(j * BN, v0);
-      if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0);
+      if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0, k1, v0, dma);
       slot_barrier(false);
-      if (kB) mma_phase(j, v1, k0); else sm_phase(j);
+      if (kB) mma_phase(j, v1, k0, k1, v0, dma); else sm_phase(j);
       slot_barrier(true);
       if (j + 1 > j1) break;
       // tile j+1: K in k1, V in v1; tile j: V in v0; tile j+2: K in k0.
-      if (j + 2 < j1) issue_k((j + 2) * BN, k0);
-      if (j + 1 < j1) issue_v((j + 1) * BN, v1);
-      if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1);
+      if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1, k0, v1, dma);
       slot_barrier(false);
-      if (kB) mma_phase(j + 1, v0, k1); else sm_phase(j + 1);
+      if (kB) mma_phase(j + 1, v0, k1, k0, v1, dma); else sm_phase(j + 1);
       slot_barrier(true);
       if (j + 2 > j1) break;
     }
