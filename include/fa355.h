@@ -187,6 +187,28 @@ typedef struct fa_paged_args {
  * paged_forward (_paged_adapter.py:15-52).  No workspace is needed. */
 int fa_paged_prefill(const fa_paged_args* args, void* stream);
 
+/* Split-KV paged prefill.  The keys of every sequence are cut into
+ * num_splits ranges (ceil(seq_len / num_splits) rounded up to 128 keys);
+ * each (query tile, KV head, range) is one workgroup writing a normalised
+ * fp32 partial and its LSE to the workspace, and a combine kernel merges
+ * the partials into out / lse.  For batches whose query tiles alone cannot
+ * fill the GPU (few new tokens against long prefixes).  Stands in for the
+ * reference's split variant (_kernels_paged.py:29-191, num_splits > 1),
+ * which its configs never enable (_kernels_paged.py:353-364) and which
+ * walks the splits sequentially inside one block.
+ *   fa_paged_prefill_num_splits: the split count paged_forward uses for
+ *     these sizes (1 = no split); reads no device data.  Negative fa_status
+ *     on invalid arguments.
+ *   fa_paged_prefill_splitkv_workspace_bytes: bytes for num_splits
+ *     (0 for num_splits == 1 or invalid arguments).
+ *   fa_paged_prefill_splitkv: num_splits in [1, 64]; 1 is fa_paged_prefill
+ *     (no workspace).  Same results as fa_paged_prefill within fp32
+ *     rounding of the merge. */
+int fa_paged_prefill_num_splits(const fa_paged_args* args);
+size_t fa_paged_prefill_splitkv_workspace_bytes(const fa_paged_args* args, int num_splits);
+int fa_paged_prefill_splitkv(const fa_paged_args* args, int num_splits, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Paged decode: one query token per sequence, split-KV + LSE-merge.        */
 /*   q, out [batch, num_heads, head_dim] (strides {batch, head})            */

@@ -256,6 +256,41 @@ def test_decode_validation_errors():
         fa.tilelang_decode_forward(q, kc, kc, bt, sl)
 
 
+def test_paged_splitkv_workspace_and_checks():
+    lib = _lib.load()
+    a = paged_args()
+    rows_per_split = a.num_heads * a.num_tokens
+    assert lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), 1) == 0
+    assert lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), 4) == \
+        4 * rows_per_split * (a.head_dim * 4 + 4) + 256
+    assert lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), 0) == 0
+    assert lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), 65) == 0
+    for ns in (0, 65, -2):
+        assert lib.fa_paged_prefill_splitkv(ctypes.byref(a), ns, None, 0, None) == \
+            _lib.FA_E_INVALID
+    # missing / short / unaligned workspace is rejected before any launch
+    need = lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), 4)
+    assert lib.fa_paged_prefill_splitkv(ctypes.byref(a), 4, None, 0, None) == _lib.FA_E_WORKSPACE
+    assert lib.fa_paged_prefill_splitkv(ctypes.byref(a), 4, 0x4000, need - 1, None) == \
+        _lib.FA_E_WORKSPACE
+    assert lib.fa_paged_prefill_splitkv(ctypes.byref(a), 4, 0x4008, need, None) == \
+        _lib.FA_E_WORKSPACE
+    assert lib.fa_paged_prefill_num_splits(ctypes.byref(paged_args(q=None))) == _lib.FA_E_INVALID
+
+
+def test_paged_num_splits_heuristic():
+    lib = _lib.load()
+    # C3-sized batch: enough query tiles to fill the GPU -> no split
+    assert lib.fa_paged_prefill_num_splits(ctypes.byref(paged_args())) == 1
+    # 64 tokens, 8 KV heads, 32k-key block table -> split, at most 16 (2048 keys each)
+    few = paged_args(num_tokens=64, batch=1, max_blocks=2048, block_table_stride=2048)
+    ns = lib.fa_paged_prefill_num_splits(ctypes.byref(few))
+    assert 2 <= ns <= 16
+    # same tokens, short block table (< 4096 keys) -> no split
+    short = paged_args(num_tokens=64, batch=1, max_blocks=128, block_table_stride=128)
+    assert lib.fa_paged_prefill_num_splits(ctypes.byref(short)) == 1
+
+
 def test_public_api_matches_reference_signatures():
     import inspect
     sig = inspect.signature(fa.tilelang_flash_attn_func)

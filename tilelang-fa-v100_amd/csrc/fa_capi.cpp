@@ -210,6 +210,46 @@ int fa_paged_prefill(const fa_paged_args* a, void* stream) {
                     "fa_paged_prefill launch");
 }
 
+int fa_paged_prefill_num_splits(const fa_paged_args* a) {
+  const int st = check_paged(a);
+  if (st != FA_OK) return st;
+  if (a->batch == 0 || a->num_tokens == 0) return 1;
+  return fa::paged_num_splits(*a);
+}
+
+static int check_splits(const fa_paged_args* a, int num_splits) {
+  if (num_splits < 1 || num_splits > fa::kMaxPagedSplits)
+    return fail(FA_E_INVALID, "fa_paged_prefill_splitkv: num_splits %d not in [1, %d]",
+                num_splits, fa::kMaxPagedSplits);
+  const int64_t grid = (int64_t)fa::paged_grid_slots(*a) * a->num_kv_heads * num_splits;
+  if (grid > kIntMax)
+    return fail(FA_E_UNSUPPORTED, "fa_paged_prefill_splitkv: problem too large");
+  return ok();
+}
+
+size_t fa_paged_prefill_splitkv_workspace_bytes(const fa_paged_args* a, int num_splits) {
+  if (check_paged(a) != FA_OK || check_splits(a, num_splits) != FA_OK) return 0;
+  return fa::paged_split_workspace_bytes(*a, num_splits);
+}
+
+int fa_paged_prefill_splitkv(const fa_paged_args* a, int num_splits, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  int st = check_paged(a);
+  if (st != FA_OK) return st;
+  st = check_splits(a, num_splits);
+  if (st != FA_OK) return st;
+  if (a->batch == 0 || a->num_tokens == 0) return ok();
+  if (a->num_pages == 0) return fail(FA_E_INVALID, "fa_paged_prefill_splitkv: empty KV cache");
+  const size_t need = fa::paged_split_workspace_bytes(*a, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(FA_E_WORKSPACE,
+                "fa_paged_prefill_splitkv: workspace needs %zu bytes (16-byte aligned), got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
+  return hip_status(fa::launch_paged_prefill_split(*a, num_splits, workspace,
+                                                   static_cast<hipStream_t>(stream)),
+                    "fa_paged_prefill_splitkv launch");
+}
+
 // ------------------------------------------------------------------ decode
 
 static int check_decode(const fa_decode_args* a) {

@@ -192,6 +192,56 @@ __device__ __forceinline__ Band mode_band(const Args& a) {
   return make_band(a);
 }
 
+// Butterfly reductions over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// Epilogue of the forward cores for one valid row: the lane holds
+// o[dt][4g + i] = O[row][32dt + 8g + 4lh + i] (unnormalised) and the row's
+// sum l_all and base-2 running max ms_run.  Writes O / l_all in the
+// input dtype and the natural-log LSE (Prob::kF32Out false), or, for
+// split-KV partials, O / l_all in fp32 and the base-2 LSE.  A row that saw
+// no key gets O = 0 and LSE = -inf.
+template <class T, int DT, class Prob>
+__device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
+                                              const f32x16 (&o)[DT], float l_all,
+                                              float ms_run) {
+  const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
+  if constexpr (Prob::kF32Out) {
+    float* op = P.o32_ptr(row);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 w = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                         o[dt][4 * g + 3] * inv};
+        *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) *P.lse2_ptr(row) = l_all > 0.f ? ms_run + log2f(l_all) : neg_inf();
+  } else {
+    uint16_t* op = P.o_ptr(row);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 w;
+        w[0] = T::pack(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
+        w[1] = T::pack(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+        st8(op + 32 * dt + 8 * g + 4 * lh, w);
+      }
+    if (P.has_lse && lh == 0)
+      *P.lse_ptr(row) = l_all > 0.f ? (ms_run + log2f(l_all)) * kLn2 : neg_inf();
+  }
+}
+
 // Instruction-scheduling hint for a loop of N steps that each issue L LDS
 // reads followed by M matrix products: the reads of the first `ahead` steps
 // go first, then every step's products are followed by the reads of step

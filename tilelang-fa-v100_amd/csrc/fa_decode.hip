@@ -41,17 +41,6 @@ struct DecShape {
 
 __host__ __device__ constexpr int dec_chunk(int D) { return 32768 / D; }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
 struct DecodeWs {
   float* po;    // [B, Hq, nsplit, D]   normalised partial outputs
   float* plse;  // [B, Hq, nsplit]      base-2 log-sum-exp of each chunk
@@ -309,7 +298,7 @@ size_t decode_workspace_bytes(const fa_decode_args& a) {
   return rows * (size_t)a.head_dim * sizeof(float) + rows * sizeof(float) + 256;
 }
 
-static int device_cu_count() {
+int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

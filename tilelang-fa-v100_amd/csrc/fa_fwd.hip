@@ -10,6 +10,8 @@
 //         scan over query_start_loc.  The Hq/Hkv query heads that share a KV
 //         head are packed into one row space (row = token * G + g), so every
 //         K/V tile fetched from the cache serves the whole GQA group.
+#include <algorithm>
+
 #include "fa_fwd_core.h"
 #include "fa_fwd_d128.h"
 #include "fa_internal.h"
@@ -29,6 +31,7 @@ struct DenseRows {
   // K / V rows are a base plus a row stride (below 2^24 elements, checked
   // by the launcher), so whole tiles can be DMA'd through buffer resources.
   static constexpr bool kRowStrided = true;
+  static constexpr bool kF32Out = false;
 
   // Row r sees keys [r + off - wl, r + off + wr] within [0, sk).
   __device__ int kv_lo(int r) const { return wl >= 0 ? min(max(r + off - wl, 0), sk) : 0; }
@@ -120,6 +123,7 @@ struct PagedRows {
   int G, nrows, seq_len, prefix, wq, wk;
   bool causal, has_lse;
   static constexpr bool kRowStrided = false;
+  static constexpr bool kF32Out = false;
 
   __device__ int kv_lo(int r) const {
     if (!causal || wq <= 0) return 0;
@@ -153,6 +157,30 @@ struct PagedRows {
   }
   __device__ const uint16_t* v_ptr(int n) const {
     return vc + page_of(n) * v_page + (n & ps_mask) * v_slot;
+  }
+};
+
+// One split of a split-KV paged prefill: the keys of the sequence are cut
+// into nsplit ranges of a multiple of 128 keys; this problem sees only keys
+// in [split_lo, split_hi) and writes its normalised partial O (fp32) and
+// base-2 LSE into the workspace at [split][head][token].
+struct PagedSplitRows : PagedRows {
+  static constexpr bool kF32Out = true;
+  int split_lo, split_hi;
+  float* po;     // [nsplit][Hq][num_tokens][D] at (split, head hk*G, token 0 of the sequence)
+  float* plse;   // [nsplit][Hq][num_tokens]    at the same origin
+  int64_t p_head;  // num_tokens
+  int D;
+
+  __device__ int kv_lo(int r) const { return max(PagedRows::kv_lo(r), split_lo); }
+  __device__ int kv_hi(int r) const { return min(PagedRows::kv_hi(r), split_hi); }
+  __device__ float* o32_ptr(int r) const {
+    const int t = r / G;
+    return po + ((r - t * G) * p_head + t) * D;
+  }
+  __device__ float* lse2_ptr(int r) const {
+    const int t = r / G;
+    return plse + (r - t * G) * p_head + t;
   }
 };
 
@@ -204,26 +232,10 @@ __device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
   return found_b;
 }
 
-template <class T, int D>
-__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
-void fwd_paged_kernel(fa_paged_args a) {
-  using S = FwdKernelCfg<D>;
+// Row problem of KV head hk of sequence b (query tokens qs .. qs+qlen-1).
+__device__ __forceinline__ void paged_rows(const fa_paged_args& a, int hk, int b, int qs,
+                                           int qlen, PagedRows& P) {
   const int G = a.num_heads / a.num_kv_heads;
-  const int slots = gridDim.x / a.num_kv_heads;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int hk = id / slots;
-  const int slot = id % slots;
-
-  int local = 0;
-  const int b = find_sequence(a.query_start_loc, a.batch, G, S::BM, slot, &local);
-  if (b < 0) return;
-  const int qs = a.query_start_loc[b];
-  const int qlen = a.query_start_loc[b + 1] - qs;
-  const int ntiles = (int)(((int64_t)qlen * G + S::BM - 1) / S::BM);
-  // Later tiles of a causal sequence see more keys: run them first.
-  const int tile = ntiles - 1 - local;
-
-  PagedRows P;
   P.G = G;
   P.nrows = qlen * G;
   P.q = static_cast<const uint16_t*>(a.q) + (int64_t)qs * a.q_stride[0] +
@@ -254,7 +266,119 @@ void fwd_paged_kernel(fa_paged_args a) {
   P.causal = a.causal != 0;
   P.wq = a.window_q;
   P.wk = a.window_k;
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+void fwd_paged_kernel(fa_paged_args a) {
+  using S = FwdKernelCfg<D>;
+  const int G = a.num_heads / a.num_kv_heads;
+  const int slots = gridDim.x / a.num_kv_heads;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int hk = id / slots;
+  const int slot = id % slots;
+
+  int local = 0;
+  const int b = find_sequence(a.query_start_loc, a.batch, G, S::BM, slot, &local);
+  if (b < 0) return;
+  const int qs = a.query_start_loc[b];
+  const int qlen = a.query_start_loc[b + 1] - qs;
+  const int ntiles = (int)(((int64_t)qlen * G + S::BM - 1) / S::BM);
+  // Later tiles of a causal sequence see more keys: run them first.
+  const int tile = ntiles - 1 - local;
+  PagedRows P;
+  paged_rows(a, hk, b, qs, qlen, P);
   run_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale);
+}
+
+// Split-KV variant: workgroup (split, KV head, tile slot); the splits of a
+// sequence cover its keys in ranges of ceil(seq_len / nsplit) rounded up to
+// 128.  Consecutive workgroup ids share the split and KV head (the same
+// K / V pages).
+template <class T, int D>
+__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+void fwd_paged_split_kernel(fa_paged_args a, int nsplit, float* po, float* plse) {
+  using S = FwdKernelCfg<D>;
+  const int G = a.num_heads / a.num_kv_heads;
+  const int per_split = gridDim.x / nsplit;
+  const int slots = per_split / a.num_kv_heads;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = id / per_split;
+  const int hk = (id % per_split) / slots;
+  const int slot = id % slots;
+
+  int local = 0;
+  const int b = find_sequence(a.query_start_loc, a.batch, G, S::BM, slot, &local);
+  if (b < 0) return;
+  const int qs = a.query_start_loc[b];
+  const int qlen = a.query_start_loc[b + 1] - qs;
+  const int ntiles = (int)(((int64_t)qlen * G + S::BM - 1) / S::BM);
+  const int tile = ntiles - 1 - local;
+  PagedSplitRows P;
+  paged_rows(a, hk, b, qs, qlen, P);
+  const int chunk = ((P.seq_len + nsplit - 1) / nsplit + 127) / 128 * 128;
+  P.split_lo = split * chunk;
+  P.split_hi = P.split_lo + chunk;
+  const int64_t origin = ((int64_t)split * a.num_heads + (int64_t)hk * G) * a.num_tokens + qs;
+  P.po = po + origin * D;
+  P.plse = plse + origin;
+  P.p_head = a.num_tokens;
+  P.D = D;
+  run_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale);
+}
+
+// Merges the nsplit partials of each (query head, token): O = sum_s w_s O_s /
+// sum_s w_s with w_s = 2^(lse_s - max); LSE = ln 2 (max + log2 sum_s w_s).
+// One wave per (head, token); tokens outside query_start_loc[0] ..
+// query_start_loc[batch] belong to no sequence and are left untouched, as
+// the unsplit kernel leaves them.
+template <class T, int D>
+__global__ __launch_bounds__(256) void paged_combine_kernel(fa_paged_args a, int nsplit,
+                                                            const float* po,
+                                                            const float* plse) {
+  constexpr int NP = (D + 127) / 128;  // d pairs per lane: 2 lane + 128 k
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t NT = a.num_tokens;
+  if (item >= (int64_t)a.num_heads * NT) return;
+  const int h = (int)(item / NT);
+  const int t = (int)(item % NT);
+  if (t < a.query_start_loc[0] || t >= a.query_start_loc[a.batch]) return;
+  const int64_t stride_s = (int64_t)a.num_heads * NT;  // rows per split
+  const int64_t row = (int64_t)h * NT + t;
+  float m = neg_inf();
+  for (int s = lane; s < nsplit; s += 64) m = fmaxf(m, plse[s * stride_s + row]);
+  m = wave_max(m);
+  const float m_use = m == neg_inf() ? 0.f : m;
+  float acc[NP][2];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) acc[k][0] = acc[k][1] = 0.f;
+  float wsum = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float ls = plse[s * stride_s + row];
+    const float w = ls == neg_inf() ? 0.f : fast_exp2(ls - m_use);
+    wsum += w;
+    const float* src = po + (s * stride_s + row) * D;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int d = 2 * lane + 128 * k;
+      if (d < D) {
+        const float2 pv = *reinterpret_cast<const float2*>(src + d);
+        acc[k][0] = fmaf(w, pv.x, acc[k][0]);
+        acc[k][1] = fmaf(w, pv.y, acc[k][1]);
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  uint16_t* op = static_cast<uint16_t*>(a.out) + (int64_t)t * a.o_stride[0] +
+                 (int64_t)h * a.o_stride[1];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int d = 2 * lane + 128 * k;
+    if (d < D)
+      *reinterpret_cast<uint32_t*>(op + d) = T::pack(acc[k][0] * inv, acc[k][1] * inv);
+  }
+  if (a.lse && lane == 0) a.lse[row] = wsum > 0.f ? (m_use + log2f(wsum)) * kLn2 : neg_inf();
 }
 
 // ----------------------------------------------------------------- launchers
@@ -306,25 +430,67 @@ int paged_grid_slots(const fa_paged_args& a) {
 }
 
 template <class T, int D>
-static hipError_t launch_paged(const fa_paged_args& a, hipStream_t st) {
-  const dim3 grid((unsigned)paged_grid_slots(a) * a.num_kv_heads);
-  hipLaunchKernelGGL((fwd_paged_kernel<T, D>), grid, dim3(FwdKernelCfg<D>::THREADS), 0, st, a);
+static hipError_t launch_paged(const fa_paged_args& a, int nsplit, void* ws, hipStream_t st) {
+  const unsigned slots = (unsigned)paged_grid_slots(a) * a.num_kv_heads;
+  if (nsplit <= 1) {
+    hipLaunchKernelGGL((fwd_paged_kernel<T, D>), dim3(slots), dim3(FwdKernelCfg<D>::THREADS), 0,
+                       st, a);
+    return hipGetLastError();
+  }
+  const size_t rows = (size_t)nsplit * a.num_heads * a.num_tokens;
+  float* po = static_cast<float*>(ws);
+  float* plse = po + rows * D;
+  hipLaunchKernelGGL((fwd_paged_split_kernel<T, D>), dim3(slots * (unsigned)nsplit),
+                     dim3(FwdKernelCfg<D>::THREADS), 0, st, a, nsplit, po, plse);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t items = (int64_t)a.num_heads * a.num_tokens;
+  hipLaunchKernelGGL((paged_combine_kernel<T, D>), dim3((unsigned)((items + 3) / 4)), dim3(256),
+                     0, st, a, nsplit, po, plse);
   return hipGetLastError();
 }
 
 template <class T>
-static hipError_t dispatch_paged_d(const fa_paged_args& a, hipStream_t st) {
+static hipError_t dispatch_paged_d(const fa_paged_args& a, int nsplit, void* ws,
+                                   hipStream_t st) {
   switch (a.head_dim) {
-    case 64: return launch_paged<T, 64>(a, st);
-    case 128: return launch_paged<T, 128>(a, st);
-    case 256: return launch_paged<T, 256>(a, st);
+    case 64: return launch_paged<T, 64>(a, nsplit, ws, st);
+    case 128: return launch_paged<T, 128>(a, nsplit, ws, st);
+    case 256: return launch_paged<T, 256>(a, nsplit, ws, st);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_paged_prefill(const fa_paged_args& a, hipStream_t st) {
-  return a.dtype == FA_DTYPE_BF16 ? dispatch_paged_d<BFloat16>(a, st)
-                                  : dispatch_paged_d<Half>(a, st);
+  return launch_paged_prefill_split(a, 1, nullptr, st);
+}
+
+hipError_t launch_paged_prefill_split(const fa_paged_args& a, int nsplit, void* ws,
+                                      hipStream_t st) {
+  return a.dtype == FA_DTYPE_BF16 ? dispatch_paged_d<BFloat16>(a, nsplit, ws, st)
+                                  : dispatch_paged_d<Half>(a, nsplit, ws, st);
+}
+
+size_t paged_split_workspace_bytes(const fa_paged_args& a, int nsplit) {
+  if (nsplit <= 1) return 0;
+  const size_t rows = (size_t)nsplit * a.num_heads * a.num_tokens;
+  return rows * a.head_dim * sizeof(float) + rows * sizeof(float) + 256;
+}
+
+// Split count from sizes alone (no device data): split only when the query
+// tiles cannot occupy the GPU (fewer workgroups than CUs) and the block
+// table can hold long sequences; each split covers at least 2048 keys.
+int paged_num_splits(const fa_paged_args& a) {
+  const int G = a.num_heads / a.num_kv_heads;
+  const int64_t tiles = ((int64_t)a.num_tokens * G + paged_block_rows(a.head_dim) - 1) /
+                        paged_block_rows(a.head_dim);
+  const int64_t wgs = std::max<int64_t>(1, tiles * a.num_kv_heads);
+  const int64_t kv_cap = (int64_t)a.max_blocks * a.page_size;
+  const int cus = device_cu_count();
+  if (wgs >= cus || kv_cap < 4096) return 1;
+  int64_t ns = (2 * (int64_t)cus + wgs - 1) / wgs;
+  ns = std::min<int64_t>(ns, kv_cap / 2048);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ns, kMaxPagedSplits));
 }
 
 }  // namespace fa

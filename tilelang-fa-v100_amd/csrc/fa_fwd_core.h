@@ -234,19 +234,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
   // Epilogue: both halves of the wave hold partial sums of the same row.
   const float l_all = l_run + swap_halves(l_run);
   if (!row_valid) return;
-  const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
-  uint16_t* op = P.o_ptr(row);
-#pragma unroll
-  for (int dt = 0; dt < S::DT; ++dt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 w;
-      w[0] = T::pack(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
-      w[1] = T::pack(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
-      st8(op + 32 * dt + 8 * g + 4 * lh, w);
-    }
-  if (P.has_lse && lh == 0)
-    *P.lse_ptr(row) = l_all > 0.f ? (ms_run + log2f(l_all)) * kLn2 : neg_inf();
+  fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
 }
 
 }  // namespace fa

@@ -16,6 +16,16 @@ hipError_t launch_bwd(const fa_bwd_args& a, void* ws, hipStream_t st);
 
 int paged_grid_slots(const fa_paged_args& a);
 hipError_t launch_paged_prefill(const fa_paged_args& a, hipStream_t st);
+// Split-KV paged prefill: nsplit in [1, kMaxPagedSplits]; ws holds
+// paged_split_workspace_bytes(a, nsplit) bytes (none for nsplit == 1).
+constexpr int kMaxPagedSplits = 64;
+int paged_num_splits(const fa_paged_args& a);
+size_t paged_split_workspace_bytes(const fa_paged_args& a, int nsplit);
+hipError_t launch_paged_prefill_split(const fa_paged_args& a, int nsplit, void* ws,
+                                      hipStream_t st);
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
 
 int decode_num_splits(const fa_decode_args& a);
 size_t decode_workspace_bytes(const fa_decode_args& a);

@@ -113,6 +113,11 @@ _PROTOTYPES = {
     "fa_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
     "fa_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
     "fa_paged_prefill": (ctypes.c_int, [ctypes.POINTER(PagedArgs), _vp]),
+    "fa_paged_prefill_num_splits": (ctypes.c_int, [ctypes.POINTER(PagedArgs)]),
+    "fa_paged_prefill_splitkv_workspace_bytes": (ctypes.c_size_t,
+                                                 [ctypes.POINTER(PagedArgs), ctypes.c_int]),
+    "fa_paged_prefill_splitkv": (ctypes.c_int, [ctypes.POINTER(PagedArgs), ctypes.c_int, _vp,
+                                                ctypes.c_size_t, _vp]),
     "fa_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "fa_paged_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
     "fa_reshape_and_cache": (ctypes.c_int, [ctypes.POINTER(CacheWriteArgs), _vp]),

@@ -9,7 +9,11 @@ Differences, all on the side of the caller:
   * softmax_lse [num_heads, num_tokens] fp32 holds the natural-log LSE of
     every query row (the reference returns an uninitialised buffer, :51);
   * fp16 and bf16 are both accepted;
-  * shape mistakes raise ValueError before any launch.
+  * shape mistakes raise ValueError before any launch;
+  * when the query tiles alone cannot fill the GPU (few new tokens, long
+    block tables), the keys are split across workgroups and merged
+    (fa_paged_prefill_splitkv; the split count comes from
+    fa_paged_prefill_num_splits).
 """
 from __future__ import annotations
 
@@ -27,6 +31,17 @@ def paged_forward(q, k_cache, v_cache, block_table, seq_lens,
                   query_start_loc, prefix_kv_lens, out=None,
                   block_size=16, num_kv_heads=None, softmax_scale=None,
                   causal=True, sliding_window_q=-1, sliding_window_k=-1):
+    return paged_forward_splits(q, k_cache, v_cache, block_table, seq_lens, query_start_loc,
+                                prefix_kv_lens, out, block_size, num_kv_heads, softmax_scale,
+                                causal, sliding_window_q, sliding_window_k)
+
+
+def paged_forward_splits(q, k_cache, v_cache, block_table, seq_lens,
+                         query_start_loc, prefix_kv_lens, out=None,
+                         block_size=16, num_kv_heads=None, softmax_scale=None,
+                         causal=True, sliding_window_q=-1, sliding_window_k=-1,
+                         num_splits=None):
+    """paged_forward with an explicit split-KV count (None: the library's)."""
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
         require_half(t, name)
     require_same({"q": q, "k_cache": k_cache, "v_cache": v_cache}, "dtype")
@@ -98,8 +113,15 @@ def paged_forward(q, k_cache, v_cache, block_table, seq_lens,
     a.dtype = _lib.dtype_code(q.dtype)
     lib = _lib.load()
     with torch.cuda.device(dev):
-        _lib.check(lib.fa_paged_prefill(ctypes.byref(a), _lib.stream_handle(dev)),
-                   "fa_paged_prefill")
+        if num_splits is None:
+            num_splits = lib.fa_paged_prefill_num_splits(ctypes.byref(a))
+            _lib.check(min(num_splits, 0), "fa_paged_prefill_num_splits")
+        nbytes = lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), int(num_splits))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
+        _lib.check(lib.fa_paged_prefill_splitkv(ctypes.byref(a), int(num_splits),
+                                                ws.data_ptr() if ws is not None else None,
+                                                nbytes, _lib.stream_handle(dev)),
+                   "fa_paged_prefill_splitkv")
     if target is not out:
         out.copy_(target)
     return out, lse
