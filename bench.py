@@ -314,6 +314,22 @@ def extras(fa, dev, reps):
     res.update([flop_entry("C5_chunked_prefill_bf16", 4 * 128 * 64 * pairs, ms, api)])
     del c
 
+    # P1: long-prefix prefill (split-KV): 2 sequences x 128 new tokens after a
+    # 32k-key prefix, 32/8 heads, D=128, fp16.  Unsplit, the query tiles
+    # give 16 workgroups; the library splits the keys.
+    from tilelang_fa_v100._paged_adapter import paged_forward_splits
+    pf = [32768, 32768]
+    g = torch.Generator().manual_seed(0)
+    c = paged_inputs([128] * 2, [p + 128 for p in pf], pf, 32, 8, 128, torch.float16, dev, g,
+                     device_values=True)
+    pairs = sum(sum(p + t + 1 for t in range(128)) for p in pf)
+    ms, api = time_reps(lambda: fa.tilelang_paged_forward(**c), reps, 3, flush)
+    ms1, api1 = time_reps(lambda: paged_forward_splits(**c, num_splits=1), reps, 3, flush)
+    res.update([flop_entry("P1_long_prefix_prefill_split", 4 * 128 * 32 * pairs, ms, api,
+                           extra={"unsplit_ms": round(ms1, 4),
+                                  "unsplit_tflops": round(4 * 128 * 32 * pairs / ms1 / 1e9, 1)})])
+    del c
+
     # C4 / T2: paged decode, batch 64, 32/8 heads, D=128
     for name, lens_fn in (("C4_decode", lambda: c4_lens()),
                           ("T2_decode_32k", lambda: ([32768] * 64, torch.Generator().manual_seed(0)))):

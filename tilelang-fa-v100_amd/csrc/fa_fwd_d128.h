@@ -228,7 +228,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   // runs the softmax (exp2, max, sums: VALU), so the two overlap instead of
   // both waves reaching the same phase together.  Group B runs one slot
   // behind group A:
-  //   slot 2j   A: O(j-1), S(j), DMA K(j+1), V(j)   B: softmax(j-1)
+  //   slot 2j   A: O(j-1), S(j)   B: softmax(j-1)   DMA: K(j+1), V(j)
   //   slot 2j+1 A: softmax(j)     B: O(j-1), S(j)   then wait for the DMA
   // K(j) is read in slots 2j, 2j+1 and V(j) in 2j+2, 2j+3, so two buffers
   // of each suffice: K(j+1) and V(j) overwrite K(j-1) and V(j-2), whose
@@ -237,17 +237,19 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   const bool grp_b = wave >= S::NW / 2;
   const int j0 = max(wg_lo, 0) / BN;
   const int j1 = (wg_hi + BN - 1) / BN;
-  // K / V tiles are DMA'd by group A alone, from inside its matrix phase:
+  // Row-strided problems (dense) DMA K / V through buffer resources: the
+  // lane's byte offset within the tile is fixed, the tile base is scalar,
+  // and rows at or past the last key read as zero (their scores are
+  // masked).  Group A alone issues them, from inside its matrix phase:
   // issuing 32 KB per tile from all eight waves at the start of a slot
   // stalled them on the vector-memory queue; behind a burst of MFMAs the
-  // queueing overlaps the matrix core's work.  Wave w < 4 fills 1 KB blocks
-  // 4w .. 4w+3 (rows 16w .. 16w+15).  Row-strided problems (dense) DMA
-  // through buffer resources: the lane's byte offset within the tile is
-  // fixed, the tile base is scalar, and rows at or past the last key read
-  // as zero (their scores are masked).  Paged problems resolve each row's
-  // page.
-  constexpr int DB = 16 / (S::NW / 2);  // blocks per DMA wave and tile
+  // queueing overlaps the matrix core's work (wave w < 4 fills 1 KB blocks
+  // 4w .. 4w+3).  Paged problems resolve each row's page with a block-table
+  // read; their DMA is spread over all eight waves (2 blocks each) at the
+  // start of the even slots, so that the table reads' latency does not
+  // stall a matrix phase.
   constexpr bool kStrided = Prob::kRowStrided;
+  constexpr int DB = kStrided ? 16 / (S::NW / 2) : 16 / S::NW;  // blocks per DMA wave
   uint32_t ld_off[DB] = {};
   if constexpr (kStrided) {
 #pragma unroll
@@ -285,9 +287,9 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
                        auto dma) {
     constexpr bool kDma = decltype(dma)::value;
     if (j - 1 >= j0 && visible((j - 1) * BN)) gemm_o(vprev);
-    if (kDma && j + 1 < j1) issue_k((j + 1) * BN, knext);
+    if (kStrided && kDma && j + 1 < j1) issue_k((j + 1) * BN, knext);
     if (j < j1 && visible(j * BN)) gemm_s(kcur);
-    if (kDma && j < j1) issue_v(j * BN, vcur);
+    if (kStrided && kDma && j < j1) issue_v(j * BN, vcur);
   };
   auto sm_phase = [&](int js) {
     if (js >= j0 && js < j1 && visible(js * BN)) softmax(js * BN);
@@ -303,7 +305,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (j0 < j1 && !grp_b) issue_k(j0 * BN, k0);
+  if (j0 < j1 && (!kStrided || !grp_b)) issue_k(j0 * BN, k0);
   wait_vmem();
   __syncthreads();
   // Each group runs its own copy of the loop (the barriers pair up across
@@ -314,12 +316,20 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     constexpr BoolC<!kB> dma{};
     for (int j = j0;; j += 2) {
       // tile j: K in k0, V in v0; tile j-1: V in v1; tile j+1: K in k1.
+      if constexpr (!kStrided) {
+        if (j + 1 < j1) issue_k((j + 1) * BN, k1);
+        if (j < j1) issue_v(j * BN, v0);
+      }
       if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0, k1, v0, dma);
       slot_barrier(false);
       if (kB) mma_phase(j, v1, k0, k1, v0, dma); else sm_phase(j);
       slot_barrier(true);
       if (j + 1 > j1) break;
       // tile j+1: K in k1, V in v1; tile j: V in v0; tile j+2: K in k0.
+      if constexpr (!kStrided) {
+        if (j + 2 < j1) issue_k((j + 2) * BN, k0);
+        if (j + 1 < j1) issue_v((j + 1) * BN, v1);
+      }
       if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1, k0, v1, dma);
       slot_barrier(false);
       if (kB) mma_phase(j + 1, v0, k1, k0, v1, dma); else sm_phase(j + 1);
