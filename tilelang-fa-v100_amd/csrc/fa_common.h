@@ -313,24 +313,33 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // otherwise, and then waits for vmcnt(0) - which also waits for every
 // outstanding global atomic.  With these forms the caller owns the wait:
 // wait_vmem() before any wave reads the target (followed by a barrier when
-// other waves read it).
+// other waves read it).  M0 (the LDS base of the DMA) is a register the
+// compiler reserves, so the statements save it and put it back.
 __device__ __forceinline__ void buffer_lds16_opaque(u32x4 rsrc, uint32_t voff, char* lds_block) {
+  uint32_t saved;
   asm volatile(
-      "s_mov_b32 m0, %2\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
-      "buffer_load_dwordx4 %0, %1, 0 offen lds"
-      :
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
       : "v"(voff), "s"(rsrc), "s"(lds_addr(lds_block))
-      : "memory", "m0");
+      : "memory");
 }
 __device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_block) {
+  uint32_t saved;
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dword %0, off"
-      :
+      "global_load_lds_dword %1, off\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
       : "v"(src), "s"(lds_addr(lds_block))
-      : "memory", "m0");
+      : "memory");
 }
 // Atomic fp32 add at base + voff + soff (no return value).
 __device__ __forceinline__ void buffer_atomic_add(rsrc_t r, uint32_t voff, uint32_t soff,

@@ -68,7 +68,10 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
   if constexpr (D == 128) {
     constexpr int B = FwdShapeD128::LDS_ARRAY_BYTES;
     __shared__ __attribute__((aligned(16))) char k0[B], v0[B], k1[B], v1[B];
-    attn_fwd_tile_d128<T>(P, row0, scale, k0, v0, k1, v1);
+    if constexpr (Prob::kRowStrided)
+      attn_fwd_tile_d128<T>(P, row0, scale, k0, v0, k1, v1);
+    else
+      attn_fwd_tile_d128_plain<T>(P, row0, scale, k0, v0, k1, v1);
   } else {
     __shared__ __attribute__((aligned(16))) uint16_t smem[FwdShape<D>::LDS_ELEMS];
     attn_fwd_tile<T, D>(P, row0, scale, smem);

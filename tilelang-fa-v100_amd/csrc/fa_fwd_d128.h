@@ -18,6 +18,9 @@
 //    i.e. all 64 banks once.
 //  * Every LDS address is precomputed per lane; tile and buffer offsets are
 //    instruction immediates.
+//  * Two schedules: attn_fwd_tile_d128_plain (all waves in the same phase,
+//    one barrier per tile; paged problems) and attn_fwd_tile_d128 (two wave
+//    groups in alternating matrix / softmax phases; dense problems).
 #pragma once
 
 #include "fa_common.h"
@@ -52,6 +55,187 @@ __device__ __forceinline__ void load_lds16(const void* g, char* lds_block) {
 // write LDS directly): vmcnt(0), expcnt/lgkmcnt untouched.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// One-phase schedule (all waves score, exponentiate and accumulate the same
+// tile between two barriers), used for paged problems: their K / V rows
+// need a block-table read each, and measured faster this way than under the
+// ping-pong schedule below (C3 0.62 vs 0.66 ms, C5 1.19 vs 1.35 ms).
+// k0/v0 and k1/v1 are four distinct __shared__ arrays of TILEB bytes.  The
+// loop is unrolled by two so that every LDS read names one array pair while
+// the DMA of the next tile targets the other; the compiler can then see that
+// the reads do not depend on the outstanding DMA and does not wait for it.
+template <class T, class Prob>
+__device__ __forceinline__ void attn_fwd_tile_d128_plain(const Prob& P, int row0, float scale,
+                                                   char* k0, char* v0, char* k1, char* v1) {
+  using S = FwdShapeD128;
+  constexpr int D = S::D, BN = S::BN;
+  const float scale_log2 = scale * kLog2e;
+  constexpr float kLazy = 8.f;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = wave_id();
+  const int lr = lane & 31, lh = lane >> 5;
+
+  const int nrows = P.nrows;
+  const int row_last = min(row0 + S::BM, nrows) - 1;
+  const int wg_lo = P.kv_lo(row0);
+  const int wg_hi = P.kv_hi(row_last);
+
+  const int wrow0 = row0 + wave * 32;
+  const bool wave_active = wrow0 < nrows;
+  const int wrow_last = min(wrow0 + 31, nrows - 1);
+  const int w_lo_min = wave_active ? P.kv_lo(wrow0) : 0;
+  const int w_lo_max = wave_active ? P.kv_lo(wrow_last) : 0;
+  const int w_hi_min = wave_active ? P.kv_hi(wrow0) : 0;
+  const int w_hi_max = wave_active ? P.kv_hi(wrow_last) : 0;
+
+  const int row = wrow0 + lr;
+  const bool row_valid = row < nrows;
+  const int my_lo = row_valid ? P.kv_lo(row) : 0;
+  const int my_hi = row_valid ? P.kv_hi(row) : 0;
+
+  u32x4 qf[D / 16];
+  {
+    const uint16_t* qp = row_valid ? P.q_ptr(row) : nullptr;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      qf[c] = row_valid ? ld16(qp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
+  }
+
+  // ---- per-lane LDS offsets (bytes, relative to a K or V tile base)
+  // K operand of Sᵀ = K Qᵀ, chunk c: row lr (+32 kt), logical chunk 2c + lh.
+  int koff[D / 16];
+  {
+    const int sw = swz_chunk(lr);
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) koff[c] = lr * S::ROWB + 16 * ((2 * c + lh) ^ sw);
+  }
+  // Vᵀ operand, 16-key chunk kc, d tile dt: lane k reads 4 halves of row
+  // 16kc + 4(k/32) + (k%16)/4 (+8 for the upper half), columns
+  // 32dt + 16((k/16)%2) + 4(k%4).  The row's swizzle does not depend on kc.
+  int voff[2][D / 32];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int r = 4 * (lane >> 5) + ((lane & 15) >> 2) + 8 * hf;
+    const int sw = swz_chunk(r);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      voff[hf][dt] = r * S::ROWB + 16 * (chunk ^ sw) + 8 * (lane & 1);
+    }
+  }
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  float ms_run = neg_inf();
+  float l_run = 0.f;
+
+  // ---- tile loader: wave w fills 1 KB blocks 2w, 2w+1 (rows 8w .. 8w+7) of
+  // the K and V tiles.  Lane l of block b holds row 4b + l/16, stored chunk
+  // l%16, i.e. logical chunk (l%16) ^ swz(row).
+  const int ld_last = max(wg_hi - 1, 0);
+  auto issue_tile = [&](int n0, char* kb, char* vb) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int blk = 2 * wave + ii;
+      const int r = 4 * blk + (lane >> 4);
+      const int c = (lane & 15) ^ swz_chunk(r);
+      const int n = min(n0 + r, ld_last);
+      load_lds16(P.k_ptr(n) + 8 * c, kb + blk * 1024);
+      load_lds16(P.v_ptr(n) + 8 * c, vb + blk * 1024);
+    }
+  };
+
+  auto compute_tile = [&](int n0, const char* kb, const char* vb) {
+    if (!(wave_active && n0 < w_hi_max && n0 + BN > w_lo_min)) return;
+    f32x16 s[BN / 32];
+#pragma unroll
+    for (int kt = 0; kt < BN / 32; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
+    // The key blocks' accumulation chains alternate (consecutive products are
+    // independent) and K reads run two chunks ahead of the products.
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int kt = 0; kt < BN / 32; ++kt)
+        s[kt] = T::mma32(ld16(kb + koff[c] + kt * 32 * S::ROWB), qf[c], s[kt]);
+    sched_pipeline<D / 16, BN / 32, BN / 32, 2>();
+    const bool need_mask = (n0 < w_lo_max) || (n0 + BN > w_hi_min);
+    if (need_mask) {
+#pragma unroll
+      for (int kt = 0; kt < BN / 32; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = n0 + kt * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+          if (kv < my_lo || kv >= my_hi) s[kt][i] = neg_inf();
+        }
+    }
+    float mt = neg_inf();
+#pragma unroll
+    for (int kt = 0; kt < BN / 32; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kt][i]);
+    mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+    const bool grow = mt > ms_run + kLazy;
+    if (__any(grow)) {
+      const float ms_new = grow ? mt : ms_run;
+      const float alpha = grow ? fast_exp2(ms_run - ms_new) : 1.f;
+      ms_run = ms_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+    }
+    const float mb = ms_run == neg_inf() ? 0.f : ms_run;
+    u32x4 pb[BN / 16];
+#pragma unroll
+    for (int kc = 0; kc < BN / 16; ++kc)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int e = 8 * (kc & 1) + 2 * w;
+        const float p0 = fast_exp2(fmaf(s[kc >> 1][e], scale_log2, -mb));
+        const float p1 = fast_exp2(fmaf(s[kc >> 1][e + 1], scale_log2, -mb));
+        pb[kc][w] = T::pack(p0, p1);
+        l_run = T::sum2(p0, p1, pb[kc][w], l_run);
+      }
+#pragma unroll
+    for (int kc = 0; kc < BN / 16; ++kc)
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const u32x2 lo = lds_read_tr(vb + voff[0][dt] + kc * 16 * S::ROWB);
+        const u32x2 hi = lds_read_tr(vb + voff[1][dt] + kc * 16 * S::ROWB);
+        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+        o[dt] = T::mma32(a, pb[kc], o[dt]);
+      }
+  };
+
+  const int j0 = max(wg_lo, 0) / BN;
+  const int j1 = (wg_hi + BN - 1) / BN;
+  if (j0 < j1) issue_tile(j0 * BN, k0, v0);
+  for (int j = j0; j < j1; j += 2) {
+    // tile j in (k0, v0)
+    wait_vmem();
+    __syncthreads();  // tile j resident; everyone is done with tile j-1
+    if (j + 1 < j1) issue_tile((j + 1) * BN, k1, v1);
+    compute_tile(j * BN, k0, v0);
+    if (j + 1 >= j1) break;
+    // tile j+1 in (k1, v1)
+    wait_vmem();
+    __syncthreads();
+    if (j + 2 < j1) issue_tile((j + 2) * BN, k0, v0);
+    compute_tile((j + 1) * BN, k1, v1);
+  }
+
+  const float l_all = l_run + swap_halves(l_run);
+  if (!row_valid) return;
+  fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
+}
+
+
+// Ping-pong schedule, used for row-strided (dense) problems.
 // k0/v0 and k1/v1 are four distinct __shared__ arrays of TILEB bytes.  The
 // loop is unrolled by two so that every LDS read names one array pair while
 // the DMA of the next tile targets the other; the compiler can then see that
@@ -124,10 +308,6 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   float ms_run = neg_inf();
   float l_run = 0.f;
 
-  // ---- tile loaders: wave w fills 1 KB blocks 2w, 2w+1 (rows 8w .. 8w+7)
-  // of a K or V tile.  Lane l of block b holds row 4b + l/16, stored chunk
-  // l%16, i.e. logical chunk (l%16) ^ swz(row).
-  const int ld_last = max(wg_hi - 1, 0);
   // Tile n0 has keys this wave's rows see.
   auto visible = [&](int n0) { return wave_active && n0 < w_hi_max && n0 + BN > w_lo_min; };
   f32x16 s[BN / 32];
@@ -228,7 +408,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   // runs the softmax (exp2, max, sums: VALU), so the two overlap instead of
   // both waves reaching the same phase together.  Group B runs one slot
   // behind group A:
-  //   slot 2j   A: O(j-1), S(j)   B: softmax(j-1)   DMA: K(j+1), V(j)
+  //   slot 2j   A: O(j-1), S(j), DMA K(j+1), V(j)   B: softmax(j-1)
   //   slot 2j+1 A: softmax(j)     B: O(j-1), S(j)   then wait for the DMA
   // K(j) is read in slots 2j, 2j+1 and V(j) in 2j+2, 2j+3, so two buffers
   // of each suffice: K(j+1) and V(j) overwrite K(j-1) and V(j-2), whose
@@ -237,46 +417,30 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   const bool grp_b = wave >= S::NW / 2;
   const int j0 = max(wg_lo, 0) / BN;
   const int j1 = (wg_hi + BN - 1) / BN;
-  // Row-strided problems (dense) DMA K / V through buffer resources: the
-  // lane's byte offset within the tile is fixed, the tile base is scalar,
-  // and rows at or past the last key read as zero (their scores are
-  // masked).  Group A alone issues them, from inside its matrix phase:
-  // issuing 32 KB per tile from all eight waves at the start of a slot
-  // stalled them on the vector-memory queue; behind a burst of MFMAs the
-  // queueing overlaps the matrix core's work (wave w < 4 fills 1 KB blocks
-  // 4w .. 4w+3).  Paged problems resolve each row's page with a block-table
-  // read; their DMA is spread over all eight waves (2 blocks each) at the
-  // start of the even slots, so that the table reads' latency does not
-  // stall a matrix phase.
-  constexpr bool kStrided = Prob::kRowStrided;
-  constexpr int DB = kStrided ? 16 / (S::NW / 2) : 16 / S::NW;  // blocks per DMA wave
-  uint32_t ld_off[DB] = {};
-  if constexpr (kStrided) {
+  // K / V rows are a base plus a row stride: tiles are DMA'd through buffer
+  // resources, the lane's byte offset within the tile is fixed, the tile
+  // base is scalar, and rows at or past the last key read as zero (their
+  // scores are masked).  Group A alone issues them, from inside its matrix
+  // phase: issuing 32 KB per tile from all eight waves at the start of a
+  // slot stalled them on the vector-memory queue; behind a burst of MFMAs
+  // the queueing overlaps the matrix core's work (wave w < 4 fills 1 KB
+  // blocks 4w .. 4w+3).
+  static_assert(Prob::kRowStrided, "ping-pong core: row-strided K / V only");
+  constexpr int DB = 16 / (S::NW / 2);  // blocks per DMA wave
+  uint32_t ld_off[DB];
 #pragma unroll
-    for (int ii = 0; ii < DB; ++ii) {
-      const int r = 4 * (DB * wave + ii) + (lane >> 4);
-      ld_off[ii] = 2u * ((uint32_t)r * (uint32_t)P.ks + 8u * ((lane & 15) ^ swz_chunk(r)));
-    }
+  for (int ii = 0; ii < DB; ++ii) {
+    const int r = 4 * (DB * wave + ii) + (lane >> 4);
+    ld_off[ii] = 2u * ((uint32_t)r * (uint32_t)P.ks + 8u * ((lane & 15) ^ swz_chunk(r)));
   }
   auto issue_rows = [&](int n0, char* dst, auto is_v) {
     constexpr bool kV = decltype(is_v)::value;
-    if constexpr (kStrided) {
-      const uint16_t* base = kV ? P.v + (int64_t)n0 * P.vs : P.k + (int64_t)n0 * P.ks;
-      const uint32_t bytes = (uint32_t)min(BN, wg_hi - n0) * (uint32_t)(kV ? P.vs : P.ks) * 2u;
-      const u32x4 rs = rsrc_words(base, bytes);
+    const uint16_t* base = kV ? P.v + (int64_t)n0 * P.vs : P.k + (int64_t)n0 * P.ks;
+    const uint32_t bytes = (uint32_t)min(BN, wg_hi - n0) * (uint32_t)(kV ? P.vs : P.ks) * 2u;
+    const u32x4 rs = rsrc_words(base, bytes);
 #pragma unroll
-      for (int ii = 0; ii < DB; ++ii)
-        buffer_lds16_opaque(rs, ld_off[ii], dst + (DB * wave + ii) * 1024);
-    } else {
-#pragma unroll
-      for (int ii = 0; ii < DB; ++ii) {
-        const int blk = DB * wave + ii;
-        const int r = 4 * blk + (lane >> 4);
-        const int c = (lane & 15) ^ swz_chunk(r);
-        const int n = min(n0 + r, ld_last);
-        load_lds16((kV ? P.v_ptr(n) : P.k_ptr(n)) + 8 * c, dst + blk * 1024);
-      }
-    }
+    for (int ii = 0; ii < DB; ++ii)
+      buffer_lds16_opaque(rs, ld_off[ii], dst + (DB * wave + ii) * 1024);
   };
   auto issue_k = [&](int n0, char* kb) { issue_rows(n0, kb, BoolC<false>{}); };
   auto issue_v = [&](int n0, char* vb) { issue_rows(n0, vb, BoolC<true>{}); };
@@ -287,9 +451,9 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
                        auto dma) {
     constexpr bool kDma = decltype(dma)::value;
     if (j - 1 >= j0 && visible((j - 1) * BN)) gemm_o(vprev);
-    if (kStrided && kDma && j + 1 < j1) issue_k((j + 1) * BN, knext);
+    if (kDma && j + 1 < j1) issue_k((j + 1) * BN, knext);
     if (j < j1 && visible(j * BN)) gemm_s(kcur);
-    if (kStrided && kDma && j < j1) issue_v(j * BN, vcur);
+    if (kDma && j < j1) issue_v(j * BN, vcur);
   };
   auto sm_phase = [&](int js) {
     if (js >= j0 && js < j1 && visible(js * BN)) softmax(js * BN);
@@ -305,7 +469,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (j0 < j1 && (!kStrided || !grp_b)) issue_k(j0 * BN, k0);
+  if (j0 < j1 && !grp_b) issue_k(j0 * BN, k0);
   wait_vmem();
   __syncthreads();
   // Each group runs its own copy of the loop (the barriers pair up across
@@ -316,20 +480,12 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     constexpr BoolC<!kB> dma{};
     for (int j = j0;; j += 2) {
       // tile j: K in k0, V in v0; tile j-1: V in v1; tile j+1: K in k1.
-      if constexpr (!kStrided) {
-        if (j + 1 < j1) issue_k((j + 1) * BN, k1);
-        if (j < j1) issue_v(j * BN, v0);
-      }
       if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0, k1, v0, dma);
       slot_barrier(false);
       if (kB) mma_phase(j, v1, k0, k1, v0, dma); else sm_phase(j);
       slot_barrier(true);
       if (j + 1 > j1) break;
       // tile j+1: K in k1, V in v1; tile j: V in v0; tile j+2: K in k0.
-      if constexpr (!kStrided) {
-        if (j + 2 < j1) issue_k((j + 2) * BN, k0);
-        if (j + 1 < j1) issue_v((j + 1) * BN, v1);
-      }
       if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1, k0, v1, dma);
       slot_barrier(false);
       if (kB) mma_phase(j + 1, v0, k1, k0, v1, dma); else sm_phase(j + 1);
