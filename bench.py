@@ -372,8 +372,10 @@ def cpu_baseline(budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # ~40 ms of untimed steps before timing: with 5 the GPU's clocks and caches had not
+    # settled (0.424 ms/step for 20 steps vs 0.389 ms/step after 50 warmup steps).
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--reps", type=int, default=20)
