@@ -173,7 +173,7 @@ typedef struct fa_paged_args {
   int32_t batch;
   int32_t num_heads;
   int32_t num_kv_heads;
-  int32_t head_dim;
+  int32_t head_dim;    /* 64, 128, 256 or 512 */
   int32_t page_size;   /* power of two */
   int32_t num_pages;
   float softmax_scale;
@@ -235,7 +235,7 @@ typedef struct fa_decode_args {
   int32_t batch;
   int32_t num_heads;
   int32_t num_kv_heads;
-  int32_t head_dim;
+  int32_t head_dim;    /* 64, 128, 256 or 512 */
   int32_t page_size;
   int32_t num_pages;
   float softmax_scale;

@@ -278,6 +278,17 @@ def test_paged_splitkv_workspace_and_checks():
     assert lib.fa_paged_prefill_num_splits(ctypes.byref(paged_args(q=None))) == _lib.FA_E_INVALID
 
 
+def test_paged_and_decode_accept_head_dim_512_dense_does_not():
+    lib = _lib.load()
+    # validation only (the rejected cases never launch)
+    assert lib.fa_paged_prefill(ctypes.byref(paged_args(head_dim=384)), None) == \
+        _lib.FA_E_UNSUPPORTED
+    assert lib.fa_paged_prefill_num_splits(ctypes.byref(paged_args(head_dim=512))) >= 1
+    assert lib.fa_fwd(ctypes.byref(fwd_args(head_dim=512)), None) == _lib.FA_E_UNSUPPORTED
+    assert lib.fa_bwd(ctypes.byref(bwd_args(head_dim=512)), 0x4000, 1 << 40, None) == \
+        _lib.FA_E_UNSUPPORTED
+
+
 def test_paged_num_splits_heuristic():
     lib = _lib.load()
     # C3-sized batch: enough query tiles to fill the GPU -> no split

@@ -75,6 +75,8 @@ GQA_ROWS = [
     (1, 8, 1, 64, 64, 256, False),
     (1, 16, 2, 32, 128, 128, True), (1, 24, 4, 32, 128, 128, True),
     (1, 8, 1, 16, 64, 256, True),
+    (1, 8, 1, 64, 64, 512, True), (1, 4, 1, 32, 160, 512, True),   # D = 512 (two O passes)
+    (1, 8, 2, 64, 64, 512, False),
 ]
 
 
@@ -97,7 +99,7 @@ def test_sliding_windows():
         check(c, causal=True, wq=wq, wk=wk)
 
 
-@pytest.mark.parametrize("page,D", [(32, 64), (1, 128), (64, 256)])
+@pytest.mark.parametrize("page,D", [(32, 64), (1, 128), (64, 256), (16, 512)])
 def test_page_sizes_and_head_dims(page, D):
     c = make_case(5, [150, 260], [400, 260], [250, 0], 4, 2, D, page=page)
     check(c, causal=True)

@@ -46,6 +46,7 @@ SPLIT_CASES = [
     ([50], [1200], [1150], 8, 1, 256, 64, torch.float16, True, 5),
     ([30, 30], [700, 400], [0, 0], 8, 2, 128, 16, torch.float16, False, 6),    # non-causal
     ([128], [4096], [3968], 64, 8, 128, 16, torch.bfloat16, True, 16),         # C5-like head count
+    ([40], [1500], [1460], 4, 1, 512, 16, torch.float16, True, 3),             # D = 512
 ]
 
 

@@ -175,8 +175,8 @@ static int check_paged(const fa_paged_args* a) {
     return fail(FA_E_INVALID, "fa_paged_prefill: null pointer");
   if (a->dtype != FA_DTYPE_F16 && a->dtype != FA_DTYPE_BF16)
     return fail(FA_E_UNSUPPORTED, "fa_paged_prefill: dtype %d not supported", a->dtype);
-  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
-    return fail(FA_E_UNSUPPORTED, "fa_paged_prefill: head_dim %d not in {64,128,256}",
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256 && a->head_dim != 512)
+    return fail(FA_E_UNSUPPORTED, "fa_paged_prefill: head_dim %d not in {64,128,256,512}",
                 a->head_dim);
   if (a->batch < 0 || a->num_tokens < 0 || a->max_blocks < 0 || a->num_pages < 0)
     return fail(FA_E_INVALID, "fa_paged_prefill: negative size");
@@ -258,8 +258,9 @@ static int check_decode(const fa_decode_args* a) {
     return fail(FA_E_INVALID, "fa_paged_decode: null pointer");
   if (a->dtype != FA_DTYPE_F16 && a->dtype != FA_DTYPE_BF16)
     return fail(FA_E_UNSUPPORTED, "fa_paged_decode: dtype %d not supported", a->dtype);
-  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
-    return fail(FA_E_UNSUPPORTED, "fa_paged_decode: head_dim %d not in {64,128,256}",
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256 &&
+      a->head_dim != 512)
+    return fail(FA_E_UNSUPPORTED, "fa_paged_decode: head_dim %d not in {64,128,256,512}",
                 a->head_dim);
   if (a->batch < 0 || a->max_blocks < 0 || a->max_seq_len < 0 || a->num_pages < 0)
     return fail(FA_E_INVALID, "fa_paged_decode: negative size");

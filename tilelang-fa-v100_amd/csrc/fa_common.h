@@ -205,7 +205,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // Epilogue of the forward cores for one valid row: the lane holds
-// o[dt][4g + i] = O[row][32dt + 8g + 4lh + i] (unnormalised) and the row's
+// o[dt][4g + i] = O[row][col0 + 32dt + 8g + 4lh + i] (unnormalised) and the row's
 // sum l_all and base-2 running max ms_run.  Writes O / l_all in the
 // input dtype and the natural-log LSE (Prob::kF32Out false), or, for
 // split-KV partials, O / l_all in fp32 and the base-2 LSE.  A row that saw
@@ -213,10 +213,10 @@ __device__ __forceinline__ float wave_sum(float x) {
 template <class T, int DT, class Prob>
 __device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
                                               const f32x16 (&o)[DT], float l_all,
-                                              float ms_run) {
+                                              float ms_run, int col0 = 0) {
   const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
   if constexpr (Prob::kF32Out) {
-    float* op = P.o32_ptr(row);
+    float* op = P.o32_ptr(row) + col0;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -227,7 +227,7 @@ __device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
       }
     if (lh == 0) *P.lse2_ptr(row) = l_all > 0.f ? ms_run + log2f(l_all) : neg_inf();
   } else {
-    uint16_t* op = P.o_ptr(row);
+    uint16_t* op = P.o_ptr(row) + col0;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll

@@ -364,6 +364,7 @@ static hipError_t launch_decode_t(const fa_decode_args& a, DecodeWs ws, hipStrea
     case 64: return launch_decode_d<T, 64>(a, ws, st);
     case 128: return launch_decode_d<T, 128>(a, ws, st);
     case 256: return launch_decode_d<T, 256>(a, ws, st);
+    case 512: return launch_decode_d<T, 512>(a, ws, st);
   }
   return hipErrorInvalidValue;
 }

@@ -460,6 +460,7 @@ static hipError_t dispatch_paged_d(const fa_paged_args& a, int nsplit, void* ws,
     case 64: return launch_paged<T, 64>(a, nsplit, ws, st);
     case 128: return launch_paged<T, 128>(a, nsplit, ws, st);
     case 256: return launch_paged<T, 256>(a, nsplit, ws, st);
+    case 512: return launch_paged<T, 512>(a, nsplit, ws, st);
   }
   return hipErrorInvalidValue;
 }

@@ -30,20 +30,31 @@ namespace fa {
 template <int D>
 struct FwdShape {
   static constexpr int BM = 128;           // query rows per workgroup
-  static constexpr int BN = 8192 / D;      // keys per tile (64 for D=128)
+  static constexpr int BN = D <= 256 ? 8192 / D : 32;  // keys per tile (64 for D=128)
   static constexpr int KS = D + 8;         // LDS row stride of K, elements
   static constexpr int VS = BN + 4;        // LDS row stride of V^T, elements
   static constexpr int KT = BN / 32;       // 32-key sub-tiles of S^T
   static constexpr int DC = D / 16;        // 16-wide d chunks (QK^T)
-  static constexpr int DT = D / 32;        // 32-wide d tiles of O^T
+  // O columns per pass: D up to 256; D = 512 runs two passes over the keys,
+  // each accumulating 256 columns of O (the scores are recomputed), so that
+  // Q, O and the tile staging fit one wave's 512 registers.
+  static constexpr int DO = D <= 256 ? D : 256;
+  static constexpr int NPASS = D / DO;
+  static constexpr int DT = DO / 32;       // 32-wide d tiles of O^T per pass
   static constexpr int KC = BN / 16;       // 16-key chunks (PV)
-  static constexpr int CPR = D / 8;        // 16-byte chunks per row
+  static constexpr int CPR = D / 8;        // 16-byte chunks per K row
   static constexpr int RSTEP = 256 / CPR;  // rows between a thread's K chunks
-  static constexpr int LDS_ELEMS = 2 * BN * KS + 2 * D * VS;
+  static constexpr int NK = BN * CPR / 256;  // 16-byte K chunks per thread per tile
+  static constexpr int CPRV = DO / 8;      // 16-byte chunks per V row and pass
+  static constexpr int RSTEPV = 256 / CPRV;
+  static constexpr int NV = BN * CPRV / 256;  // 16-byte V chunks per thread per tile
+  static constexpr int VG = 4 * RSTEPV;    // keys between a thread's groups of 4 V rows
+  static constexpr int LDS_ELEMS = 2 * BN * KS + 2 * DO * VS;
   // Two workgroups per CU (2 waves per SIMD) fit the register file up to D=128.
   static constexpr int kWavesPerEU = D <= 128 ? 2 : 1;
   static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
-  static_assert(BN * CPR == 4 * 256, "four 16-byte chunks per thread per tile");
+  static_assert(NV % 4 == 0 && BN % VG == 0 && NK * 256 == BN * CPR,
+                "whole groups of four V rows per thread");
 };
 
 // Prob must provide:
@@ -63,7 +74,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
   const int lr = lane & 31, lh = lane >> 5;
 
   uint16_t* Ks = smem;                    // [2][BN][KS]
-  uint16_t* Vt = smem + 2 * S::BN * S::KS;  // [2][D][VS]
+  uint16_t* Vt = smem + 2 * S::BN * S::KS;  // [2][DO][VS]
 
   const int nrows = P.nrows;
   const int row_last = min(row0 + S::BM, nrows) - 1;
@@ -93,19 +104,17 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
   }
 
   f32x16 o[S::DT];
-#pragma unroll
-  for (int dt = 0; dt < S::DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-  float ms_run = neg_inf();  // running row max * scale * log2(e)
-  float l_run = 0.f;
+  float ms_run, l_run;  // running row max * scale * log2(e), running row sum
 
   // Cooperative tile loader: thread t owns the 16-byte column chunk
   // col8 = t % CPR; K rows r0 + i*RSTEP and V rows 4*r0 + i (four consecutive
   // keys, so V can be transposed in registers before the LDS store).
   const int col8 = tid % S::CPR;
   const int r0 = tid / S::CPR;
-  u32x4 kreg[4], vreg[4];
+  const int col8v = tid % S::CPRV;
+  const int r0v = tid / S::CPRV;
+  u32x4 kreg[S::NK], vreg[S::NV];
+  int vcol = 0;  // first O / V column of the pass
   // Rows at or beyond wg_hi are never visible: they are loaded from the last
   // visible row instead (finite data, multiplied by P = 0), which keeps every
   // load unconditional and never touches memory past the keys.
@@ -113,39 +122,50 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
 
   auto load_tile = [&](int n0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < S::NK; ++i) {
       const int n = min(n0 + r0 + i * S::RSTEP, ld_last);
       kreg[i] = ld16(P.k_ptr(n) + col8 * 8);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = min(n0 + 4 * r0 + i, ld_last);
-      vreg[i] = ld16(P.v_ptr(n) + col8 * 8);
+    for (int i = 0; i < S::NV; ++i) {
+      const int n = min(n0 + (i / 4) * S::VG + 4 * r0v + (i % 4), ld_last);
+      vreg[i] = ld16(P.v_ptr(n) + vcol + col8v * 8);
     }
   };
   auto store_tile = [&](int buf) {
     uint16_t* kb = Ks + buf * S::BN * S::KS;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < S::NK; ++i)
       st16(kb + (r0 + i * S::RSTEP) * S::KS + col8 * 8, kreg[i]);
-    uint16_t* vb = Vt + buf * D * S::VS;
+    uint16_t* vb = Vt + buf * S::DO * S::VS;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int w = j >> 1;
-      u32x2 pr;
-      if (j & 1) {
-        pr[0] = pack_hi(vreg[0][w], vreg[1][w]);
-        pr[1] = pack_hi(vreg[2][w], vreg[3][w]);
-      } else {
-        pr[0] = pack_lo(vreg[0][w], vreg[1][w]);
-        pr[1] = pack_lo(vreg[2][w], vreg[3][w]);
+    for (int gi = 0; gi < S::NV / 4; ++gi)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int w = j >> 1;
+        const u32x4* vg = vreg + 4 * gi;
+        u32x2 pr;
+        if (j & 1) {
+          pr[0] = pack_hi(vg[0][w], vg[1][w]);
+          pr[1] = pack_hi(vg[2][w], vg[3][w]);
+        } else {
+          pr[0] = pack_lo(vg[0][w], vg[1][w]);
+          pr[1] = pack_lo(vg[2][w], vg[3][w]);
+        }
+        st8(vb + (col8v * 8 + j) * S::VS + gi * S::VG + 4 * r0v, pr);
       }
-      st8(vb + (col8 * 8 + j) * S::VS + 4 * r0, pr);
-    }
   };
 
   const int j0 = max(wg_lo, 0) / S::BN;
   const int j1 = (wg_hi + S::BN - 1) / S::BN;
+  for (int pass = 0; pass < S::NPASS; ++pass) {
+  vcol = pass * S::DO;
+#pragma unroll
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  ms_run = neg_inf();
+  l_run = 0.f;
   if (j0 < j1) {
     load_tile(j0 * S::BN);
     store_tile(0);
@@ -157,7 +177,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
       const int n0 = j * S::BN;
       if (wave_active && n0 < w_hi_max && n0 + S::BN > w_lo_min) {
         const uint16_t* kb = Ks + buf * S::BN * S::KS;
-        const uint16_t* vb = Vt + buf * D * S::VS;
+        const uint16_t* vb = Vt + buf * S::DO * S::VS;
         f32x16 s[S::KT];
 #pragma unroll
         for (int kt = 0; kt < S::KT; ++kt) {
@@ -232,9 +252,10 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
   }
 
   // Epilogue: both halves of the wave hold partial sums of the same row.
+  // (No early return: a second pass still takes part in the barriers.)
   const float l_all = l_run + swap_halves(l_run);
-  if (!row_valid) return;
-  fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
+  if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run, vcol);
+  }  // pass
 }
 
 }  // namespace fa

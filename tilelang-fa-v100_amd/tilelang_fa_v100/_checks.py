@@ -9,7 +9,8 @@ from __future__ import annotations
 import torch
 
 _FLOAT16 = (torch.float16, torch.bfloat16)
-HEAD_DIMS = (64, 128, 256)
+HEAD_DIMS = (64, 128, 256)             # dense forward / backward
+PAGED_HEAD_DIMS = (64, 128, 256, 512)  # paged prefill and decode (_kernels_paged.py:353-364)
 
 
 def require_cuda(t: torch.Tensor, name: str) -> None:

@@ -23,7 +23,7 @@ import math
 import torch
 
 from . import _lib
-from ._checks import (HEAD_DIMS, as_int32, require_cuda, require_half, require_same,
+from ._checks import (PAGED_HEAD_DIMS, as_int32, require_cuda, require_half, require_same,
                       rows_ready, strides)
 
 
@@ -58,8 +58,8 @@ def paged_forward_splits(q, k_cache, v_cache, block_table, seq_lens,
         raise ValueError(f"num_kv_heads {heads_kv} != k_cache heads {cache_heads}")
     if cache_d != D:
         raise ValueError(f"head_dim mismatch: q {D}, cache {cache_d}")
-    if D not in HEAD_DIMS:
-        raise ValueError(f"head_dim {D} not supported (expected one of {HEAD_DIMS})")
+    if D not in PAGED_HEAD_DIMS:
+        raise ValueError(f"head_dim {D} not supported (expected one of {PAGED_HEAD_DIMS})")
     if num_heads % heads_kv != 0:
         raise ValueError(f"num_heads {num_heads} is not a multiple of num_kv_heads {heads_kv}")
     if page_size <= 0 or page_size & (page_size - 1):
