@@ -402,18 +402,21 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   };
 
   // Ping-pong schedule.  Waves 0-3 (group A) and 4-7 (group B) share the
-  // SIMDs pairwise; the loop runs in slots separated by workgroup barriers,
-  // and in every slot one wave of each SIMD runs matrix products (Oᵀ of the
-  // previous tile, then Sᵀ of the current one: 32 MFMAs) while the other
-  // runs the softmax (exp2, max, sums: VALU), so the two overlap instead of
-  // both waves reaching the same phase together.  Group B runs one slot
-  // behind group A:
-  //   slot 2j   A: O(j-1), S(j), DMA K(j+1), V(j)   B: softmax(j-1)
-  //   slot 2j+1 A: softmax(j)     B: O(j-1), S(j)   then wait for the DMA
-  // K(j) is read in slots 2j, 2j+1 and V(j) in 2j+2, 2j+3, so two buffers
-  // of each suffice: K(j+1) and V(j) overwrite K(j-1) and V(j-2), whose
-  // last reads were in slot 2j-1.  The loop body covers two tiles so that
-  // every buffer is a compile-time array (see the note on k0..v1 above).
+  // SIMDs pairwise; between two workgroup barriers (one per tile) each wave
+  // runs two phases in opposite order to its partner, so one wave of each
+  // SIMD runs matrix products (Oᵀ of the previous tile, then Sᵀ of the
+  // current one: 32 MFMAs) while the other runs the softmax (exp2, max,
+  // sums: VALU), instead of both waves reaching the same phase together.
+  // Group B runs one phase behind group A (a barrier between the two phases
+  // as well measured 2% slower):
+  //   period j:  A: O(j-1), S(j), DMA K(j+1), V(j); then softmax(j)
+  //              B: softmax(j-1); then O(j-1), S(j)
+  //              wait for the DMA, barrier
+  // K(j) is read in period j and V(j) in period j+1, so two buffers of each
+  // suffice: K(j+1) and V(j) overwrite K(j-1) and V(j-2), whose last reads
+  // were in period j-1, before its barrier.  The loop body covers two tiles
+  // so that every buffer is a compile-time array (see the note on k0..v1
+  // above).
   const bool grp_b = wave >= S::NW / 2;
   const int j0 = max(wg_lo, 0) / BN;
   const int j1 = (wg_hi + BN - 1) / BN;
@@ -458,14 +461,12 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   auto sm_phase = [&](int js) {
     if (js >= j0 && js < j1 && visible(js * BN)) softmax(js * BN);
   };
-  auto slot_barrier = [&](bool wait_dma) {
+  // Wait for this wave's DMA, then the workgroup barrier that makes every
+  // wave's DMA visible and frees the buffers read before it.
+  auto tile_barrier = [&]() {
     __builtin_amdgcn_sched_barrier(0);
-    if (wait_dma) {
-      wait_vmem();
-      __syncthreads();
-    } else {
-      __builtin_amdgcn_s_barrier();
-    }
+    wait_vmem();
+    __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -481,15 +482,13 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     for (int j = j0;; j += 2) {
       // tile j: K in k0, V in v0; tile j-1: V in v1; tile j+1: K in k1.
       if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0, k1, v0, dma);
-      slot_barrier(false);
       if (kB) mma_phase(j, v1, k0, k1, v0, dma); else sm_phase(j);
-      slot_barrier(true);
+      tile_barrier();
       if (j + 1 > j1) break;
       // tile j+1: K in k1, V in v1; tile j: V in v0; tile j+2: K in k0.
       if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1, k0, v1, dma);
-      slot_barrier(false);
       if (kB) mma_phase(j + 1, v0, k1, k0, v1, dma); else sm_phase(j + 1);
-      slot_barrier(true);
+      tile_barrier();
       if (j + 2 > j1) break;
     }
   };
