@@ -53,42 +53,62 @@ struct BwdShape {
 };
 
 // ------------------------------------------------------------ preprocess
+// Grid (query blocks, B*H): block (x, bh) covers rows q = kPreRowsPerBlock x
+// .. +kPreRowsPerBlock-1 of (batch, head) bh, so the statistics and the dQ
+// accumulator ([B, H, Sq, D]) are written contiguously and no lane divides.
+// LPR lanes (16 bytes of O and dO each) per row, kPreRows rows per lane
+// group, all loads issued first.
+constexpr int kPreRows = 4;
+
+template <int D>
+constexpr int pre_rows_per_block() { return 256 / (D / 8) * kPreRows; }
+
 template <class T, int D>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqacc,
                                                       float* stats) {
-  constexpr int LPR = D / 8;          // lanes per row
-  constexpr int RPB = 256 / LPR;      // rows per block
-  const int64_t nrows = (int64_t)a.batch * a.seqlen_q * a.num_heads;
-  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  constexpr int LPR = D / 8;     // lanes per row
+  constexpr int RPP = 256 / LPR;  // rows per pass of the block
+  const int Sq = a.seqlen_q, H = a.num_heads;
+  const int bh = blockIdx.y;
+  const int h = bh % H, b = bh / H;
+  const int q0 = blockIdx.x * pre_rows_per_block<D>() + threadIdx.x / LPR;
   const int sub = threadIdx.x % LPR;
-  float acc = 0.f;
-  int b = 0, q = 0, h = 0;
-  if (r < nrows) {
-    h = (int)(r % a.num_heads);
-    const int64_t bq = r / a.num_heads;
-    q = (int)(bq % a.seqlen_q);
-    b = (int)(bq / a.seqlen_q);
-    const uint16_t* op = static_cast<const uint16_t*>(a.out) + b * a.o_stride[0] +
-                         q * a.o_stride[1] + h * a.o_stride[2] + 8 * sub;
-    const uint16_t* dp = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
-                         q * a.do_stride[1] + h * a.do_stride[2] + 8 * sub;
-    const u32x4 ov = ld16(op), dv = ld16(dp);
+  const uint16_t* ob = static_cast<const uint16_t*>(a.out) + b * a.o_stride[0] +
+                       h * a.o_stride[2] + 8 * sub;
+  const uint16_t* db = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
+                       h * a.do_stride[2] + 8 * sub;
+  u32x4 ov[kPreRows], dv[kPreRows];
+#pragma unroll
+  for (int p = 0; p < kPreRows; ++p) {
+    const int q = q0 + p * RPP;
+    ov[p] = dv[p] = u32x4{0, 0, 0, 0};
+    if (q < Sq) {
+      ov[p] = ld16(ob + (int64_t)q * a.o_stride[1]);
+      dv[p] = ld16(db + (int64_t)q * a.do_stride[1]);
+    }
+  }
+  const int64_t row0 = (int64_t)bh * Sq;
+#pragma unroll
+  for (int p = 0; p < kPreRows; ++p) {
+    const int q = q0 + p * RPP;
+    float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-      acc += T::lo(ov[w]) * T::lo(dv[w]) + T::hi(ov[w]) * T::hi(dv[w]);
-    float* z = dqacc + r * D + 8 * sub;
-    st16(z, u32x4{0, 0, 0, 0});
-    st16(z + 4, u32x4{0, 0, 0, 0});
-  }
+      acc += T::lo(ov[p][w]) * T::lo(dv[p][w]) + T::hi(ov[p][w]) * T::hi(dv[p][w]);
 #pragma unroll
-  for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
-  if (r < nrows && sub == 0) {
-    const int64_t bh = (int64_t)b * a.num_heads + h;
-    const float l = a.lse[bh * a.seqlen_q + q];
-    float* st = stats + 2 * bh * a.seqlen_q + q;
-    // A row that saw no key has lse = -inf; +inf makes its P exactly zero.
-    st[0] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
-    st[a.seqlen_q] = acc;
+    for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    if (q < Sq) {
+      float* z = dqacc + (row0 + q) * D + 8 * sub;
+      st16(z, u32x4{0, 0, 0, 0});
+      st16(z + 4, u32x4{0, 0, 0, 0});
+      if (sub == 0) {
+        const float l = a.lse[row0 + q];
+        float* st = stats + 2 * row0 + q;
+        // A row that saw no key has lse = -inf; +inf makes its P exactly zero.
+        st[0] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
+        st[Sq] = acc;
+      }
+    }
   }
 }
 
@@ -381,31 +401,43 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
 }
 
 // ------------------------------------------------------------ dQ convert
+// Same row order and lane split as bwd_pre_kernel: reads of the accumulator
+// are contiguous.
 template <class T, int D>
 __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(fa_bwd_args a,
                                                              const float* dqacc) {
   constexpr int LPR = D / 8;
-  constexpr int RPB = 256 / LPR;
-  const int64_t nrows = (int64_t)a.batch * a.seqlen_q * a.num_heads;
-  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  constexpr int RPP = 256 / LPR;
+  const int Sq = a.seqlen_q, H = a.num_heads;
+  const int bh = blockIdx.y;
+  const int h = bh % H, b = bh / H;
+  const int q0 = blockIdx.x * pre_rows_per_block<D>() + threadIdx.x / LPR;
   const int sub = threadIdx.x % LPR;
-  if (r >= nrows) return;
-  const int h = (int)(r % a.num_heads);
-  const int64_t bq = r / a.num_heads;
-  const int q = (int)(bq % a.seqlen_q);
-  const int b = (int)(bq / a.seqlen_q);
-  const float* src = dqacc + (((int64_t)b * a.num_heads + h) * a.seqlen_q + q) * D + 8 * sub;
-  const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
-  const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
+  const int64_t row0 = (int64_t)bh * Sq;
+  f32x4 x0[kPreRows], x1[kPreRows];
+#pragma unroll
+  for (int p = 0; p < kPreRows; ++p) {
+    const int q = q0 + p * RPP;
+    if (q < Sq) {
+      const float* src = dqacc + (row0 + q) * D + 8 * sub;
+      x0[p] = *reinterpret_cast<const f32x4*>(src);
+      x1[p] = *reinterpret_cast<const f32x4*>(src + 4);
+    }
+  }
   const float sc = a.softmax_scale;
-  u32x4 w;
-  w[0] = T::pack(x0[0] * sc, x0[1] * sc);
-  w[1] = T::pack(x0[2] * sc, x0[3] * sc);
-  w[2] = T::pack(x1[0] * sc, x1[1] * sc);
-  w[3] = T::pack(x1[2] * sc, x1[3] * sc);
-  uint16_t* dst = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] + q * a.dq_stride[1] +
-                  h * a.dq_stride[2] + 8 * sub;
-  st16(dst, w);
+#pragma unroll
+  for (int p = 0; p < kPreRows; ++p) {
+    const int q = q0 + p * RPP;
+    if (q >= Sq) continue;
+    u32x4 w;
+    w[0] = T::pack(x0[p][0] * sc, x0[p][1] * sc);
+    w[1] = T::pack(x0[p][2] * sc, x0[p][3] * sc);
+    w[2] = T::pack(x1[p][0] * sc, x1[p][1] * sc);
+    w[3] = T::pack(x1[p][2] * sc, x1[p][3] * sc);
+    uint16_t* dst = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] +
+                    (int64_t)q * a.dq_stride[1] + h * a.dq_stride[2] + 8 * sub;
+    st16(dst, w);
+  }
 }
 
 // ----------------------------------------------------------------- launchers
@@ -420,8 +452,8 @@ static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
   float* dqacc = static_cast<float*>(ws);
   float* stats = dqacc + rows * D;  // [B*H][2][Sq]
-  constexpr int RPB = 256 / (D / 8);
-  const dim3 rgrid((unsigned)((rows + RPB - 1) / RPB));
+  const dim3 rgrid((unsigned)((a.seqlen_q + pre_rows_per_block<D>() - 1) / pre_rows_per_block<D>()),
+                   (unsigned)(a.batch * a.num_heads));
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

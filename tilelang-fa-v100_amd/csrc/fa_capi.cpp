@@ -146,6 +146,9 @@ static int check_bwd(const fa_bwd_args* a) {
   const int64_t rows = (int64_t)a->batch * a->seqlen_q * a->num_heads;
   if (tiles > kIntMax || rows / 16 > kIntMax)
     return fail(FA_E_UNSUPPORTED, "fa_bwd: problem too large");
+  // The row pre/post-processing kernels index (batch, head) by grid y.
+  if ((int64_t)a->batch * a->num_heads > 65535)
+    return fail(FA_E_UNSUPPORTED, "fa_bwd: batch * num_heads must be at most 65535");
   return ok();
 }
 
