@@ -31,8 +31,8 @@ namespace fa {
 
 template <int D>
 struct BwdShape {
-  static constexpr int BKV = 128;         // keys per workgroup
-  static constexpr int BQ = 64;           // query rows per iteration
+  static constexpr int BKV = tiles::kBwd64Keys;       // keys per workgroup
+  static constexpr int BQ = tiles::kBwd64QueryRows;   // query rows per iteration
   static constexpr int NQT = BQ / 32;     // 32-row query sub-tiles
   static constexpr int DC = D / 16;       // 16-wide d chunks (QK^T, dO V^T)
   static constexpr int DT = D / 32;       // 32-wide d tiles (dK^T, dV^T, dQ)
@@ -58,7 +58,7 @@ struct BwdShape {
 // accumulator ([B, H, Sq, D]) are written contiguously and no lane divides.
 // LPR lanes (16 bytes of O and dO each) per row, kPreRows rows per lane
 // group, all loads issued first.
-constexpr int kPreRows = 4;
+constexpr int kPreRows = tiles::kBwdPreRows;
 
 template <int D>
 constexpr int pre_rows_per_block() { return 256 / (D / 8) * kPreRows; }

@@ -43,7 +43,7 @@ struct BwdShapeMfma {
   static constexpr int D = D_;
   static constexpr int NW = D == 128 ? 8 / KB : 4;  // waves per workgroup
   static constexpr int BKV = 32 * KB * NW;  // keys per workgroup: 256 (D=128), 128 (D=256)
-  static constexpr int BQ = 32;             // query rows per iteration
+  static constexpr int BQ = tiles::kBwdQueryRows;  // query rows per iteration
   static constexpr int ROWB = 2 * D;        // bytes per K / Q / dO row
   static constexpr int CPR = D / 8;         // 16-byte chunks per row
   static constexpr int RPB = 1024 / ROWB;   // rows per 1 KB DMA block
@@ -62,7 +62,7 @@ struct BwdShapeMfma {
 };
 
 // Key blocks per wave used by the launcher.
-constexpr int kBwdKB = 1;
+constexpr int kBwdKB = tiles::kBwd128KeyBlocksPerWave;
 
 // MODE (MaskMode): full attention, causal, or a window band from the arguments.
 template <class T, int D_, int MODE, int KB>

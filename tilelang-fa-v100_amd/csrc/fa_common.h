@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "fa355.h"
+#include "fa_tiles.h"
 
 namespace fa {
 

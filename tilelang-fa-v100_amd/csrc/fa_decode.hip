@@ -29,7 +29,7 @@ namespace fa {
 // 16 bytes (32768 / D keys for any D), all loads issued before any use.
 template <int D>
 struct DecShape {
-  static constexpr int CH = 32768 / D;   // keys per chunk (256 for D=128)
+  static constexpr int CH = tiles::kDecChunkElems / D;  // keys per chunk (256 for D=128)
   static constexpr int DC = D / 32;      // 32-wide d chunks of the QK^T MFMA
   static constexpr int KIT = CH / 64;    // 16-key blocks per wave (phase 1)
   static constexpr int LPT = D / 8;      // lanes per V row (phase 3)
@@ -39,7 +39,7 @@ struct DecShape {
   static_assert(KIT * DC == 16 && VIT == 16, "16 K and 16 V loads per lane");
 };
 
-__host__ __device__ constexpr int dec_chunk(int D) { return 32768 / D; }
+__host__ __device__ constexpr int dec_chunk(int D) { return tiles::kDecChunkElems / D; }
 
 struct DecodeWs {
   float* po;    // [B, Hq, nsplit, D]   normalised partial outputs

@@ -39,9 +39,9 @@ namespace fa {
 
 struct DecStream {
   static constexpr int D = 128;
-  static constexpr int kSplit = 512;   // keys per item / partial
-  static constexpr int kTile = 16;     // keys per tile
-  static constexpr int kDepth = 2;     // tiles in the per-wave LDS ring
+  static constexpr int kSplit = tiles::kDecSplitKeys;      // keys per item / partial
+  static constexpr int kTile = tiles::kDecTileKeys;        // keys per tile
+  static constexpr int kDepth = tiles::kDecTilesInFlight;  // tiles in the per-wave LDS ring
   static constexpr int kMaxBatch = 1024;
   static constexpr int kWavesPerCU = 8;
   static constexpr int kWavesPerWG = 8;

@@ -491,9 +491,9 @@ int paged_num_splits(const fa_paged_args& a) {
   const int64_t wgs = std::max<int64_t>(1, tiles * a.num_kv_heads);
   const int64_t kv_cap = (int64_t)a.max_blocks * a.page_size;
   const int cus = device_cu_count();
-  if (wgs >= cus || kv_cap < 4096) return 1;
+  if (wgs >= cus || kv_cap < tiles::kSplitMinKeys) return 1;
   int64_t ns = (2 * (int64_t)cus + wgs - 1) / wgs;
-  ns = std::min<int64_t>(ns, kv_cap / 2048);
+  ns = std::min<int64_t>(ns, kv_cap / tiles::kSplitKeysPerRange);
   return (int)std::max<int64_t>(1, std::min<int64_t>(ns, kMaxPagedSplits));
 }
 

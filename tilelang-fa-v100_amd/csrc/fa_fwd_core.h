@@ -29,8 +29,9 @@ namespace fa {
 
 template <int D>
 struct FwdShape {
-  static constexpr int BM = 128;           // query rows per workgroup
-  static constexpr int BN = D <= 256 ? 8192 / D : 32;  // keys per tile (64 for D=128)
+  static constexpr int BM = tiles::kFwdCoreRows;  // query rows per workgroup
+  // keys per tile (64 for D=128)
+  static constexpr int BN = D <= 256 ? tiles::kFwdCoreTileElems / D : tiles::kFwdCoreKeys512;
   static constexpr int KS = D + 8;         // LDS row stride of K, elements
   static constexpr int VS = BN + 4;        // LDS row stride of V^T, elements
   static constexpr int KT = BN / 32;       // 32-key sub-tiles of S^T

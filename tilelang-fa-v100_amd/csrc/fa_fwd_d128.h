@@ -29,9 +29,9 @@ namespace fa {
 
 struct FwdShapeD128 {
   static constexpr int D = 128;
-  static constexpr int BM = 256;          // query rows per workgroup
-  static constexpr int BN = 64;           // keys per tile
-  static constexpr int NW = 8;            // waves
+  static constexpr int BM = tiles::kFwd128Rows;   // query rows per workgroup
+  static constexpr int BN = tiles::kFwd128Keys;   // keys per tile
+  static constexpr int NW = tiles::kFwd128Waves;  // waves
   static constexpr int ROWB = 256;        // bytes per K/V row
   static constexpr int TILEB = BN * ROWB; // 16 KB per K or V tile
   static constexpr int LDS_BYTES = 2 * 2 * TILEB;  // 2 buffers x (K, V)

@@ -6,6 +6,7 @@
 #include <stddef.h>
 
 #include "fa355.h"
+#include "fa_tiles.h"
 
 namespace fa {
 
@@ -18,7 +19,7 @@ int paged_grid_slots(const fa_paged_args& a);
 hipError_t launch_paged_prefill(const fa_paged_args& a, hipStream_t st);
 // Split-KV paged prefill: nsplit in [1, kMaxPagedSplits]; ws holds
 // paged_split_workspace_bytes(a, nsplit) bytes (none for nsplit == 1).
-constexpr int kMaxPagedSplits = 64;
+constexpr int kMaxPagedSplits = tiles::kMaxSplits;
 int paged_num_splits(const fa_paged_args& a);
 size_t paged_split_workspace_bytes(const fa_paged_args& a, int nsplit);
 hipError_t launch_paged_prefill_split(const fa_paged_args& a, int nsplit, void* ws,

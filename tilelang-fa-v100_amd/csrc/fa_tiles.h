@@ -1,0 +1,85 @@
+// Fixed gfx950 tile table.
+//
+// Replaces the reference's run-time autotuner (tilelang_fa_v100/_configs.py:5-79
+// candidate generators, _utils.py:4-27 SM70 validity model, the fixed
+// _BEST_CONFIGS / _DECODE_BEST_CONFIGS dicts in _kernels_paged.py:353-364,
+// 495-499).  Every kernel takes its tile sizes from here; nothing is tuned at
+// run time, so the first call of a shape costs no compilation or search.
+// Each entry states the measurement (MI355X, rocprofv3 counters or event
+// timing of T1 = causal fp16 B=2 S=8192 H=16 D=128, C2 = the same at B=4
+// S=2048) that chose it over the alternatives tried.
+#pragma once
+
+namespace fa {
+namespace tiles {
+
+// ---- dense / paged forward, head_dim 128 (fa_fwd_d128.h)
+// 256 query rows per workgroup = 8 waves x 32 rows (two waves per SIMD, 207
+// VGPRs, no spills), 64-key K/V tiles double-buffered in LDS (64 KB).
+// Evidence: T1 forward 0.545 ms, MFMA busy 52.5% (SQ_VALU_MFMA_BUSY_CYCLES);
+// 4-wave / 128-row workgroups (two per CU) measured 0.673 ms against 0.640 ms
+// for this shape under the same (one-phase) schedule; LDS bank conflicts 0
+// (SQ_LDS_BANK_CONFLICT) with the 16-byte chunk swizzle.
+constexpr int kFwd128Rows = 256;
+constexpr int kFwd128Keys = 64;
+constexpr int kFwd128Waves = 8;
+
+// ---- forward, head_dim 64 / 256 / 512 (fa_fwd_core.h)
+// 128 query rows per workgroup (4 waves x 32 rows); keys per tile
+// 8192 / D for D <= 256 (a 16 KB K tile), 32 for D = 512, whose O columns are
+// accumulated in two 256-wide passes so Q, O and the staging fit one wave's
+// 512 registers; 2 waves per SIMD for D <= 128, 1 above.
+// Evidence (compiler resource usage): D = 64 takes 182 VGPRs and D = 256
+// 254 VGPRs + 152 AGPRs (one wave per SIMD), both without spills; D = 512
+// (two O passes) 512 registers with 35 spilled.  C1 (D = 64) is launch-bound
+// (13.5 us), so its tile is sized for occupancy, not peak rate.
+constexpr int kFwdCoreRows = 128;
+constexpr int kFwdCoreTileElems = 8192;  // keys x head_dim per K tile (D <= 256)
+constexpr int kFwdCoreKeys512 = 32;
+
+// ---- backward main kernel, head_dim 128 / 256 (fa_bwd_mfma.h)
+// KV-stationary: head_dim 128 keeps 256 keys per workgroup (8 waves x 32 keys,
+// dK / dV of a wave's 32 keys in 128 registers), head_dim 256 keeps 128 keys
+// (4 waves); 32 query rows per iteration.
+// Evidence: the dQ atomics cost 0.36-0.44 ms of T1's 1.78 ms backward and their
+// count is inverse to the keys per workgroup, so the largest key tile whose
+// dK / dV fit the register file wins; 4 waves x 64 keys (512 registers each)
+// measured slower (accumulator traffic); MFMA busy 38.1% on T1.
+constexpr int kBwd128KeyBlocksPerWave = 1;
+constexpr int kBwdQueryRows = 32;
+
+// ---- backward main kernel, head_dim 64 (fa_bwd.hip)
+// 128 keys per workgroup, 64 query rows per iteration, 4 waves.
+constexpr int kBwd64Keys = 128;
+constexpr int kBwd64QueryRows = 64;
+
+// ---- backward row kernels (fa_bwd.hip): 4 rows per lane group (D / 8
+// lanes per row) with all their loads issued together.  Evidence: C2 pre
+// 28.2 us and convert 15.9 us (kernel trace), 4.8 and 6.3 TB/s.
+constexpr int kBwdPreRows = 4;
+
+// ---- decode, head_dim 128 (fa_decode_stream.h)
+// Persistent waves; work item = 512-key split x one KV head x its query heads
+// (up to 8, the 16x16x32 MFMA columns); 16-key tiles, two in flight per wave.
+// Evidence: T2 (32k context) reads 1.006x its algorithmic bytes
+// (FETCH_SIZE) at 73% of 8 TB/s.
+constexpr int kDecSplitKeys = 512;
+constexpr int kDecTileKeys = 16;
+constexpr int kDecTilesInFlight = 2;
+
+// ---- decode, head_dim 64 / 256 / 512 (fa_decode.hip): 32768 elements
+// (64 KB) of K per chunk, i.e. 32768 / D keys.
+constexpr int kDecChunkElems = 32768;
+
+// ---- split-KV paged prefill (fa_fwd.hip paged_num_splits): no split when
+// the query tiles alone give >= CU-count workgroups or the block table holds
+// fewer than kSplitMinKeys keys; otherwise ceil(2 x CUs / workgroups)
+// ranges of at least kSplitKeysPerRange keys, at most kMaxSplits.
+// Evidence: P1 (2 x 128 tokens after a 32k prefix) 0.21 ms split against
+// 1.01 ms unsplit.
+constexpr int kSplitMinKeys = 4096;
+constexpr int kSplitKeysPerRange = 2048;
+constexpr int kMaxSplits = 64;
+
+}  // namespace tiles
+}  // namespace fa
