@@ -71,6 +71,20 @@ def test_forward_reads_strided_packed_qkv():
     assert_close(out, r_out)
 
 
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_forward_k_and_v_with_different_row_strides(D):
+    # K dense, V a column slice of a wider tensor: the two row strides differ,
+    # and the D = 128 core DMAs K and V rows with per-lane offsets of each.
+    g = torch.Generator().manual_seed(3)
+    q = randn(g, 1, 333, 4, D).to(DEV)
+    k = randn(g, 1, 333, 2, D).to(DEV)
+    v = randn(g, 1, 333, 2, D + 64).to(DEV)[..., :D]
+    assert k.stride(1) != v.stride(1)
+    out = fa.tilelang_flash_attn_func(q, k, v, causal=True)
+    r_out, _ = ref.dense_attention(q.cpu(), k.cpu(), v.cpu().contiguous(), causal=True)
+    assert_close(out, r_out)
+
+
 BWD_CASES = [
     (4, 2048, 2048, 16, 16, 128, True, torch.float16),
     (2, 200, 200, 4, 4, 64, False, torch.float16),

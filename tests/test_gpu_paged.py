@@ -99,7 +99,7 @@ def test_sliding_windows():
         check(c, causal=True, wq=wq, wk=wk)
 
 
-@pytest.mark.parametrize("page,D", [(32, 64), (1, 128), (64, 256), (16, 512)])
+@pytest.mark.parametrize("page,D", [(32, 64), (1, 128), (32, 128), (128, 128), (64, 256), (16, 512)])
 def test_page_sizes_and_head_dims(page, D):
     c = make_case(5, [150, 260], [400, 260], [250, 0], 4, 2, D, page=page)
     check(c, causal=True)

@@ -30,7 +30,6 @@ struct DenseRows {
   bool has_lse;
   // K / V rows are a base plus a row stride (below 2^24 elements, checked
   // by the launcher), so whole tiles can be DMA'd through buffer resources.
-  static constexpr bool kRowStrided = true;
   static constexpr bool kF32Out = false;
 
   // Row r sees keys [r + off - wl, r + off + wr] within [0, sk).
@@ -43,6 +42,8 @@ struct DenseRows {
   __device__ float* lse_ptr(int r) const { return lse + r; }
   __device__ const uint16_t* k_ptr(int n) const { return k + n * ks; }
   __device__ const uint16_t* v_ptr(int n) const { return v + n * vs; }
+  __device__ int64_t k_row_stride() const { return ks; }
+  __device__ int64_t v_row_stride() const { return vs; }
 };
 
 // Tile geometry per head_dim: D = 128 uses the direct-to-LDS 8-wave core.
@@ -62,13 +63,16 @@ struct FwdKernelCfg<128> {
 };
 
 // LDS: one array for the 4-wave core; four distinct arrays for the D = 128
-// core (see attn_fwd_tile_d128).
-template <class T, int D, class Prob>
+// cores (see attn_fwd_tile_d128).  PP: the ping-pong D = 128 core, which
+// needs 16 consecutive keys at a fixed row stride (dense rows, or pages of
+// at least 16 keys) with row strides below 2^24 elements; otherwise the
+// one-phase core.
+template <class T, int D, bool PP, class Prob>
 __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scale) {
   if constexpr (D == 128) {
     constexpr int B = FwdShapeD128::LDS_ARRAY_BYTES;
     __shared__ __attribute__((aligned(16))) char k0[B], v0[B], k1[B], v1[B];
-    if constexpr (Prob::kRowStrided)
+    if constexpr (PP)
       attn_fwd_tile_d128<T>(P, row0, scale, k0, v0, k1, v1);
     else
       attn_fwd_tile_d128_plain<T>(P, row0, scale, k0, v0, k1, v1);
@@ -110,7 +114,7 @@ void fwd_dense_kernel(fa_fwd_args a) {
   P.wl = band.wl;
   P.wr = band.wr;
   P.has_lse = a.lse != nullptr;
-  run_fwd_tile<T, D>(P, qt * C::BM, a.softmax_scale);
+  run_fwd_tile<T, D, true>(P, qt * C::BM, a.softmax_scale);
 }
 
 struct PagedRows {
@@ -125,7 +129,6 @@ struct PagedRows {
   int ps_log2, ps_mask, last_page;
   int G, nrows, seq_len, prefix, wq, wk;
   bool causal, has_lse;
-  static constexpr bool kRowStrided = false;
   static constexpr bool kF32Out = false;
 
   __device__ int kv_lo(int r) const {
@@ -161,6 +164,9 @@ struct PagedRows {
   __device__ const uint16_t* v_ptr(int n) const {
     return vc + page_of(n) * v_page + (n & ps_mask) * v_slot;
   }
+  // Stride between consecutive keys of one page.
+  __device__ int64_t k_row_stride() const { return k_slot; }
+  __device__ int64_t v_row_stride() const { return v_slot; }
 };
 
 // One split of a split-KV paged prefill: the keys of the sequence are cut
@@ -271,7 +277,7 @@ __device__ __forceinline__ void paged_rows(const fa_paged_args& a, int hk, int b
   P.wk = a.window_k;
 }
 
-template <class T, int D>
+template <class T, int D, bool PP>
 __global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
 void fwd_paged_kernel(fa_paged_args a) {
   using S = FwdKernelCfg<D>;
@@ -291,14 +297,14 @@ void fwd_paged_kernel(fa_paged_args a) {
   const int tile = ntiles - 1 - local;
   PagedRows P;
   paged_rows(a, hk, b, qs, qlen, P);
-  run_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale);
+  run_fwd_tile<T, D, PP>(P, tile * S::BM, a.softmax_scale);
 }
 
 // Split-KV variant: workgroup (split, KV head, tile slot); the splits of a
 // sequence cover its keys in ranges of ceil(seq_len / nsplit) rounded up to
 // 128.  Consecutive workgroup ids share the split and KV head (the same
 // K / V pages).
-template <class T, int D>
+template <class T, int D, bool PP>
 __global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
 void fwd_paged_split_kernel(fa_paged_args a, int nsplit, float* po, float* plse) {
   using S = FwdKernelCfg<D>;
@@ -327,7 +333,7 @@ void fwd_paged_split_kernel(fa_paged_args a, int nsplit, float* po, float* plse)
   P.plse = plse + origin;
   P.p_head = a.num_tokens;
   P.D = D;
-  run_fwd_tile<T, D>(P, tile * S::BM, a.softmax_scale);
+  run_fwd_tile<T, D, PP>(P, tile * S::BM, a.softmax_scale);
 }
 
 // Merges the nsplit partials of each (query head, token): O = sum_s w_s O_s /
@@ -432,18 +438,26 @@ int paged_grid_slots(const fa_paged_args& a) {
   return (int)((rows + bm - 1) / bm + a.batch);
 }
 
-template <class T, int D>
-static hipError_t launch_paged(const fa_paged_args& a, int nsplit, void* ws, hipStream_t st) {
+// The ping-pong D = 128 core takes K / V in runs of 16 keys at a fixed row
+// stride: pages of at least 16 keys, token strides below 2^24 elements.
+static bool paged_pingpong(const fa_paged_args& a) {
+  const int64_t lim = int64_t(1) << 24;
+  return a.head_dim == 128 && a.page_size >= 16 && a.k_stride[1] < lim && a.v_stride[1] < lim;
+}
+
+template <class T, int D, bool PP>
+static hipError_t launch_paged_pp(const fa_paged_args& a, int nsplit, void* ws,
+                                  hipStream_t st) {
   const unsigned slots = (unsigned)paged_grid_slots(a) * a.num_kv_heads;
   if (nsplit <= 1) {
-    hipLaunchKernelGGL((fwd_paged_kernel<T, D>), dim3(slots), dim3(FwdKernelCfg<D>::THREADS), 0,
-                       st, a);
+    hipLaunchKernelGGL((fwd_paged_kernel<T, D, PP>), dim3(slots),
+                       dim3(FwdKernelCfg<D>::THREADS), 0, st, a);
     return hipGetLastError();
   }
   const size_t rows = (size_t)nsplit * a.num_heads * a.num_tokens;
   float* po = static_cast<float*>(ws);
   float* plse = po + rows * D;
-  hipLaunchKernelGGL((fwd_paged_split_kernel<T, D>), dim3(slots * (unsigned)nsplit),
+  hipLaunchKernelGGL((fwd_paged_split_kernel<T, D, PP>), dim3(slots * (unsigned)nsplit),
                      dim3(FwdKernelCfg<D>::THREADS), 0, st, a, nsplit, po, plse);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -451,6 +465,14 @@ static hipError_t launch_paged(const fa_paged_args& a, int nsplit, void* ws, hip
   hipLaunchKernelGGL((paged_combine_kernel<T, D>), dim3((unsigned)((items + 3) / 4)), dim3(256),
                      0, st, a, nsplit, po, plse);
   return hipGetLastError();
+}
+
+template <class T, int D>
+static hipError_t launch_paged(const fa_paged_args& a, int nsplit, void* ws, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (paged_pingpong(a)) return launch_paged_pp<T, D, true>(a, nsplit, ws, st);
+  }
+  return launch_paged_pp<T, D, false>(a, nsplit, ws, st);
 }
 
 template <class T>

@@ -427,23 +427,37 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   // phase: issuing 32 KB per tile from all eight waves at the start of a
   // slot stalled them on the vector-memory queue; behind a burst of MFMAs
   // the queueing overlaps the matrix core's work (wave w < 4 fills 1 KB
-  // blocks 4w .. 4w+3).
-  static_assert(Prob::kRowStrided, "ping-pong core: row-strided K / V only");
+  // blocks 4w .. 4w+3, i.e. keys n0 + 16w .. n0 + 16w + 15).  A wave's 16
+  // rows are a base plus the row stride: for paged K / V (pages of at least
+  // 16 keys) they lie in one page, whose block-table entry is one scalar
+  // load per wave and tile.
   constexpr int DB = 16 / (S::NW / 2);  // blocks per DMA wave
-  uint32_t ld_off[DB];
+  static_assert(DB * 4 == 16, "each DMA wave fills 16 rows");
+  uint32_t k_loff[DB], v_loff[DB];
 #pragma unroll
   for (int ii = 0; ii < DB; ++ii) {
-    const int r = 4 * (DB * wave + ii) + (lane >> 4);
-    ld_off[ii] = 2u * ((uint32_t)r * (uint32_t)P.ks + 8u * ((lane & 15) ^ swz_chunk(r)));
+    const int r = 4 * (DB * wave + ii) + (lane >> 4);  // row of the tile
+    const uint32_t r16 = 4 * ii + (lane >> 4);         // row of the wave's 16
+    const uint32_t chunk = 8u * ((lane & 15) ^ swz_chunk(r));
+    k_loff[ii] = 2u * (r16 * (uint32_t)P.k_row_stride() + chunk);
+    v_loff[ii] = 2u * (r16 * (uint32_t)P.v_row_stride() + chunk);
   }
   auto issue_rows = [&](int n0, char* dst, auto is_v) {
     constexpr bool kV = decltype(is_v)::value;
-    const uint16_t* base = kV ? P.v + (int64_t)n0 * P.vs : P.k + (int64_t)n0 * P.ks;
-    const uint32_t bytes = (uint32_t)min(BN, wg_hi - n0) * (uint32_t)(kV ? P.vs : P.ks) * 2u;
-    const u32x4 rs = rsrc_words(base, bytes);
+    const int nw = n0 + 16 * wave;
+    const int nvalid = min(16, wg_hi - nw);  // n0 < wg_hi, so n0's row resolves
+    const int nb = nvalid > 0 ? nw : n0;
+    const uint16_t* base = kV ? P.v_ptr(nb) : P.k_ptr(nb);
+    const uint32_t bytes =
+        (uint32_t)max(nvalid, 0) * (uint32_t)(kV ? P.v_row_stride() : P.k_row_stride()) * 2u;
+    u32x4 rs = rsrc_words(base, bytes);
+    // Uniform by construction (the block-table read of a paged problem is
+    // not known to be); the resource must sit in scalar registers.
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(rs[w]);
 #pragma unroll
     for (int ii = 0; ii < DB; ++ii)
-      buffer_lds16_opaque(rs, ld_off[ii], dst + (DB * wave + ii) * 1024);
+      buffer_lds16_opaque(rs, kV ? v_loff[ii] : k_loff[ii], dst + (DB * wave + ii) * 1024);
   };
   auto issue_k = [&](int n0, char* kb) { issue_rows(n0, kb, BoolC<false>{}); };
   auto issue_v = [&](int n0, char* vb) { issue_rows(n0, vb, BoolC<true>{}); };
