@@ -18,9 +18,10 @@
 //    i.e. all 64 banks once.
 //  * Every LDS address is precomputed per lane; tile and buffer offsets are
 //    instruction immediates.
-//  * Two schedules: attn_fwd_tile_d128_plain (all waves in the same phase,
-//    one barrier per tile; paged problems) and attn_fwd_tile_d128 (two wave
-//    groups in alternating matrix / softmax phases; dense problems).
+//  * Two schedules: attn_fwd_tile_d128 (two wave groups in alternating
+//    matrix / softmax phases; dense problems and paged problems whose pages
+//    hold at least 16 keys) and attn_fwd_tile_d128_plain (all waves in the
+//    same phase, one barrier per tile; paged problems with smaller pages).
 #pragma once
 
 #include "fa_common.h"
@@ -56,9 +57,9 @@ __device__ __forceinline__ void load_lds16(const void* g, char* lds_block) {
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // One-phase schedule (all waves score, exponentiate and accumulate the same
-// tile between two barriers), used for paged problems: their K / V rows
-// need a block-table read each, and measured faster this way than under the
-// ping-pong schedule below (C3 0.62 vs 0.66 ms, C5 1.19 vs 1.35 ms).
+// tile between two barriers), used for paged problems whose pages hold fewer
+// than 16 keys: their K / V rows need a block-table read each (the ping-pong
+// schedule below takes 16-key runs at a fixed stride).
 // k0/v0 and k1/v1 are four distinct __shared__ arrays of TILEB bytes.  The
 // loop is unrolled by two so that every LDS read names one array pair while
 // the DMA of the next tile targets the other; the compiler can then see that
