@@ -14,6 +14,7 @@
 
 #include "fa_fwd_core.h"
 #include "fa_fwd_d128.h"
+#include "fa_fwd_d256.h"
 #include "fa_internal.h"
 
 namespace fa {
@@ -46,8 +47,10 @@ struct DenseRows {
   __device__ int64_t v_row_stride() const { return vs; }
 };
 
-// Tile geometry per head_dim: D = 128 uses the direct-to-LDS 8-wave core.
-template <int D>
+// Tile geometry per head_dim and core: D = 128 (both schedules) and D = 256
+// with PP (two-phase schedule) use the direct-to-LDS 8-wave cores, the rest
+// the 4-wave core.
+template <int D, bool PP>
 struct FwdKernelCfg {
   static constexpr int BM = FwdShape<D>::BM;
   static constexpr int THREADS = 256;
@@ -55,7 +58,14 @@ struct FwdKernelCfg {
   static constexpr int LDS_BYTES = FwdShape<D>::LDS_ELEMS * 2;
 };
 template <>
-struct FwdKernelCfg<128> {
+struct FwdKernelCfg<256, true> {
+  static constexpr int BM = FwdShapeD256::BM;
+  static constexpr int THREADS = 512;
+  static constexpr int WAVES_PER_EU = 2;
+  static constexpr int LDS_BYTES = FwdShapeD256::LDS_BYTES;
+};
+template <bool PP>
+struct FwdKernelCfg<128, PP> {
   static constexpr int BM = FwdShapeD128::BM;
   static constexpr int THREADS = 512;
   static constexpr int WAVES_PER_EU = 2;
@@ -76,6 +86,11 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
       attn_fwd_tile_d128<T>(P, row0, scale, k0, v0, k1, v1);
     else
       attn_fwd_tile_d128_plain<T>(P, row0, scale, k0, v0, k1, v1);
+  } else if constexpr (D == 256 && PP) {
+    using S = FwdShapeD256;
+    __shared__ __attribute__((aligned(16))) char k0[S::KTILEB], v0[S::VTILEB], k1[S::KTILEB],
+        v1[S::VTILEB];
+    attn_fwd_tile_d256<T>(P, row0, scale, k0, v0, k1, v1);
   } else {
     __shared__ __attribute__((aligned(16))) uint16_t smem[FwdShape<D>::LDS_ELEMS];
     attn_fwd_tile<T, D>(P, row0, scale, smem);
@@ -85,9 +100,10 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
 // MODE (MaskMode): full attention, causal, or a window band from the
 // arguments.  The causal and full bands are compile-time constants.
 template <class T, int D, int MODE>
-__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+__global__ __launch_bounds__((FwdKernelCfg<D, true>::THREADS),
+                             (FwdKernelCfg<D, true>::WAVES_PER_EU))
 void fwd_dense_kernel(fa_fwd_args a) {
-  using C = FwdKernelCfg<D>;
+  using C = FwdKernelCfg<D, true>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const TileHead th = xcd_tile_order(blockIdx.x, qtiles, a.batch * a.num_heads);
   const int bh = th.bh;
@@ -278,9 +294,9 @@ __device__ __forceinline__ void paged_rows(const fa_paged_args& a, int hk, int b
 }
 
 template <class T, int D, bool PP>
-__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+__global__ __launch_bounds__((FwdKernelCfg<D, PP>::THREADS), (FwdKernelCfg<D, PP>::WAVES_PER_EU))
 void fwd_paged_kernel(fa_paged_args a) {
-  using S = FwdKernelCfg<D>;
+  using S = FwdKernelCfg<D, PP>;
   const int G = a.num_heads / a.num_kv_heads;
   const int slots = gridDim.x / a.num_kv_heads;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -305,9 +321,9 @@ void fwd_paged_kernel(fa_paged_args a) {
 // 128.  Consecutive workgroup ids share the split and KV head (the same
 // K / V pages).
 template <class T, int D, bool PP>
-__global__ __launch_bounds__(FwdKernelCfg<D>::THREADS, FwdKernelCfg<D>::WAVES_PER_EU)
+__global__ __launch_bounds__((FwdKernelCfg<D, PP>::THREADS), (FwdKernelCfg<D, PP>::WAVES_PER_EU))
 void fwd_paged_split_kernel(fa_paged_args a, int nsplit, float* po, float* plse) {
-  using S = FwdKernelCfg<D>;
+  using S = FwdKernelCfg<D, PP>;
   const int G = a.num_heads / a.num_kv_heads;
   const int per_split = gridDim.x / nsplit;
   const int slots = per_split / a.num_kv_heads;
@@ -394,7 +410,7 @@ __global__ __launch_bounds__(256) void paged_combine_kernel(fa_paged_args a, int
 
 template <class T, int D>
 static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
-  using C = FwdKernelCfg<D>;
+  using C = FwdKernelCfg<D, true>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
   const int mode = mask_mode(a);
@@ -422,27 +438,31 @@ hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st) {
                                   : dispatch_dense_d<Half>(a, st);
 }
 
-int paged_block_rows(int head_dim) {
-  switch (head_dim) {
-    case 64: return FwdKernelCfg<64>::BM;
-    case 128: return FwdKernelCfg<128>::BM;
-    default: return FwdKernelCfg<256>::BM;
+// The two-phase D = 128 / 256 cores take K / V in runs of 16 (D = 128) or
+// 8 (D = 256) keys at a fixed row stride: pages of at least 16 keys, token
+// strides below 2^24 elements.
+static bool paged_pingpong(const fa_paged_args& a) {
+  const int64_t lim = int64_t(1) << 24;
+  return (a.head_dim == 128 || a.head_dim == 256) && a.page_size >= 16 &&
+         a.k_stride[1] < lim && a.v_stride[1] < lim;
+}
+
+int paged_block_rows(const fa_paged_args& a) {
+  const bool pp = paged_pingpong(a);
+  switch (a.head_dim) {
+    case 64: return FwdKernelCfg<64, false>::BM;
+    case 128: return FwdKernelCfg<128, false>::BM;
+    case 256: return pp ? FwdKernelCfg<256, true>::BM : FwdKernelCfg<256, false>::BM;
+    default: return FwdKernelCfg<512, false>::BM;
   }
 }
 
 int paged_grid_slots(const fa_paged_args& a) {
   const int G = a.num_heads / a.num_kv_heads;
   const int64_t rows = (int64_t)a.num_tokens * G;
-  const int bm = paged_block_rows(a.head_dim);
+  const int bm = paged_block_rows(a);
   // sum_b ceil(rows_b / BM) <= ceil(rows / BM) + batch
   return (int)((rows + bm - 1) / bm + a.batch);
-}
-
-// The ping-pong D = 128 core takes K / V in runs of 16 keys at a fixed row
-// stride: pages of at least 16 keys, token strides below 2^24 elements.
-static bool paged_pingpong(const fa_paged_args& a) {
-  const int64_t lim = int64_t(1) << 24;
-  return a.head_dim == 128 && a.page_size >= 16 && a.k_stride[1] < lim && a.v_stride[1] < lim;
 }
 
 template <class T, int D, bool PP>
@@ -451,14 +471,14 @@ static hipError_t launch_paged_pp(const fa_paged_args& a, int nsplit, void* ws,
   const unsigned slots = (unsigned)paged_grid_slots(a) * a.num_kv_heads;
   if (nsplit <= 1) {
     hipLaunchKernelGGL((fwd_paged_kernel<T, D, PP>), dim3(slots),
-                       dim3(FwdKernelCfg<D>::THREADS), 0, st, a);
+                       dim3(FwdKernelCfg<D, PP>::THREADS), 0, st, a);
     return hipGetLastError();
   }
   const size_t rows = (size_t)nsplit * a.num_heads * a.num_tokens;
   float* po = static_cast<float*>(ws);
   float* plse = po + rows * D;
   hipLaunchKernelGGL((fwd_paged_split_kernel<T, D, PP>), dim3(slots * (unsigned)nsplit),
-                     dim3(FwdKernelCfg<D>::THREADS), 0, st, a, nsplit, po, plse);
+                     dim3(FwdKernelCfg<D, PP>::THREADS), 0, st, a, nsplit, po, plse);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t items = (int64_t)a.num_heads * a.num_tokens;
@@ -469,7 +489,7 @@ static hipError_t launch_paged_pp(const fa_paged_args& a, int nsplit, void* ws,
 
 template <class T, int D>
 static hipError_t launch_paged(const fa_paged_args& a, int nsplit, void* ws, hipStream_t st) {
-  if constexpr (D == 128) {
+  if constexpr (D == 128 || D == 256) {
     if (paged_pingpong(a)) return launch_paged_pp<T, D, true>(a, nsplit, ws, st);
   }
   return launch_paged_pp<T, D, false>(a, nsplit, ws, st);
@@ -508,8 +528,8 @@ size_t paged_split_workspace_bytes(const fa_paged_args& a, int nsplit) {
 // table can hold long sequences; each split covers at least 2048 keys.
 int paged_num_splits(const fa_paged_args& a) {
   const int G = a.num_heads / a.num_kv_heads;
-  const int64_t tiles = ((int64_t)a.num_tokens * G + paged_block_rows(a.head_dim) - 1) /
-                        paged_block_rows(a.head_dim);
+  const int64_t tiles =
+      ((int64_t)a.num_tokens * G + paged_block_rows(a) - 1) / paged_block_rows(a);
   const int64_t wgs = std::max<int64_t>(1, tiles * a.num_kv_heads);
   const int64_t kv_cap = (int64_t)a.max_blocks * a.page_size;
   const int cus = device_cu_count();

@@ -24,7 +24,18 @@ constexpr int kFwd128Rows = 256;
 constexpr int kFwd128Keys = 64;
 constexpr int kFwd128Waves = 8;
 
-// ---- forward, head_dim 64 / 256 / 512 (fa_fwd_core.h)
+// ---- dense / paged forward, head_dim 256 (fa_fwd_d256.h)
+// The head_dim 128 schedule with 32-key tiles and O in two 128-column passes
+// (the scores recomputed), so two waves fit each SIMD (230 VGPRs, no
+// spills).  Evidence: T1 shape at head_dim 256 (B=2, S=8192, H=8, causal)
+// 0.844 ms against 1.204 ms for the one-pass 4-wave core (406 registers,
+// one wave per SIMD), despite 1.5x the matrix products.
+constexpr int kFwd256Rows = 256;
+constexpr int kFwd256Keys = 32;
+constexpr int kFwd256Waves = 8;
+
+// ---- forward, head_dim 64 / 256 / 512 (fa_fwd_core.h; head_dim 256 only for
+// paged problems with pages of fewer than 16 keys)
 // 128 query rows per workgroup (4 waves x 32 rows); keys per tile
 // 8192 / D for D <= 256 (a 16 KB K tile), 32 for D = 512, whose O columns are
 // accumulated in two 256-wide passes so Q, O and the staging fit one wave's
