@@ -93,8 +93,9 @@ def test_mixed_batch_noncausal_and_empty_sequences():
     check(c, causal=True)
 
 
-def test_sliding_windows():
-    c = make_case(4, [200, 77], [500, 77], [300, 0], 8, 4, 128)
+@pytest.mark.parametrize("D", [128, 256])
+def test_sliding_windows(D):
+    c = make_case(4, [200, 77], [500, 77], [300, 0], 8, 4, D)
     for wq, wk in ((64, -1), (-1, 33), (100, 50), (1, -1)):
         check(c, causal=True, wq=wq, wk=wk)
 
