@@ -321,7 +321,8 @@ def extras(fa, dev, reps):
 
     # P1: long-prefix prefill (split-KV): 2 sequences x 128 new tokens after a
     # 32k-key prefix, 32/8 heads, D=128, fp16.  Unsplit, the query tiles
-    # give 16 workgroups; the library splits the keys.
+    # give 32 workgroups (2 x 4 row tiles x 8 KV heads); the library splits
+    # the keys.
     from tilelang_fa_v100._paged_adapter import paged_forward_splits
     pf = [32768, 32768]
     g = torch.Generator().manual_seed(0)

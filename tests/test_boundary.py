@@ -297,10 +297,18 @@ def test_paged_num_splits_heuristic():
     lib = _lib.load()
     # C3-sized batch: enough query tiles to fill the GPU -> no split
     assert lib.fa_paged_prefill_num_splits(ctypes.byref(paged_args())) == 1
-    # 64 tokens, 8 KV heads, 32k-key block table -> split, at most 16 (2048 keys each)
+    # 64 tokens, 8 KV heads (8 workgroups), 32k-key block table -> split:
+    # about one workgroup per CU (256 CUs without a GPU), ranges of 1024-8192 keys
     few = paged_args(num_tokens=64, batch=1, max_blocks=2048, block_table_stride=2048)
     ns = lib.fa_paged_prefill_num_splits(ctypes.byref(few))
-    assert 2 <= ns <= 16
+    assert ns == 32
+    # 256 tokens x 4 heads per KV head = 4 row tiles, x 8 KV heads = 32 workgroups;
+    # 8k-key table: max(256 / 32, 1) = 8 ranges of 1024 keys
+    mid = paged_args(num_tokens=256, batch=1, max_blocks=512, block_table_stride=512)
+    assert lib.fa_paged_prefill_num_splits(ctypes.byref(mid)) == 8
+    # 64k-key table: max(8, 8) = 8; 128k keys: max(8, 16) = 16 (ranges of at most 8192 keys)
+    big = paged_args(num_tokens=256, batch=1, max_blocks=8192, block_table_stride=8192)
+    assert lib.fa_paged_prefill_num_splits(ctypes.byref(big)) == 16
     # same tokens, short block table (< 4096 keys) -> no split
     short = paged_args(num_tokens=64, batch=1, max_blocks=128, block_table_stride=128)
     assert lib.fa_paged_prefill_num_splits(ctypes.byref(short)) == 1

@@ -534,8 +534,12 @@ int paged_num_splits(const fa_paged_args& a) {
   const int64_t kv_cap = (int64_t)a.max_blocks * a.page_size;
   const int cus = device_cu_count();
   if (wgs >= cus || kv_cap < tiles::kSplitMinKeys) return 1;
-  int64_t ns = (2 * (int64_t)cus + wgs - 1) / wgs;
-  ns = std::min<int64_t>(ns, kv_cap / tiles::kSplitKeysPerRange);
+  // About one workgroup per CU, and no range longer than kSplitMaxRangeKeys
+  // (a workgroup's serial length), but none shorter than kSplitMinRangeKeys
+  // (each split adds a partial O per row to write and merge).
+  int64_t ns = std::max<int64_t>((cus + wgs - 1) / wgs,
+                                 (kv_cap + tiles::kSplitMaxRangeKeys - 1) / tiles::kSplitMaxRangeKeys);
+  ns = std::min<int64_t>(ns, kv_cap / tiles::kSplitMinRangeKeys);
   return (int)std::max<int64_t>(1, std::min<int64_t>(ns, kMaxPagedSplits));
 }
 

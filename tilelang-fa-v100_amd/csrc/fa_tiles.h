@@ -84,12 +84,18 @@ constexpr int kDecChunkElems = 32768;
 
 // ---- split-KV paged prefill (fa_fwd.hip paged_num_splits): no split when
 // the query tiles alone give >= CU-count workgroups or the block table holds
-// fewer than kSplitMinKeys keys; otherwise ceil(2 x CUs / workgroups)
-// ranges of at least kSplitKeysPerRange keys, at most kMaxSplits.
-// Evidence: P1 (2 x 128 tokens after a 32k prefix) 0.21 ms split against
-// 1.01 ms unsplit.
+// fewer than kSplitMinKeys keys; otherwise max(ceil(CUs / workgroups),
+// ceil(keys / kSplitMaxRangeKeys)) ranges, but none shorter than
+// kSplitMinRangeKeys and at most kMaxSplits.
+// Evidence (2 sequences, 32 / 8 heads, D = 128, time per call in ms for
+// 1 / 4 / 8 / 16 splits): 32k-key prefix + 128 tokens 0.955 / 0.277 / 0.171 /
+// 0.192 (this rule: 8); 16k + 128: 0.487 / 0.153 / 0.104 / 0.128 (8);
+// 32k + 512: 0.994 / 0.593 / 0.634 / 0.729 (5); 8k + 64: 0.252 / 0.087 /
+// 0.062 / 0.080 (8).  The former rule (2 x CUs / workgroups ranges of at
+// least 2048 keys) chose 16, 8, 4 and 4.
 constexpr int kSplitMinKeys = 4096;
-constexpr int kSplitKeysPerRange = 2048;
+constexpr int kSplitMinRangeKeys = 1024;
+constexpr int kSplitMaxRangeKeys = 8192;
 constexpr int kMaxSplits = 64;
 
 }  // namespace tiles
