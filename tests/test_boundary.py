@@ -189,8 +189,14 @@ def decode_args(**over):
 def test_decode_workspace_and_checks():
     lib = _lib.load()
     a = decode_args()
-    rows = 64 * 32 * (32768 // 512)  # D=128, page >= 16: 512-key splits
+    # D=128, page >= 16: the streaming kernel; 64 x 16 x 8 items of 2048 keys are
+    # >= 2 per resident wave (256 CUs x 8 waves without a GPU): 2048-key splits
+    rows = 64 * 32 * (32768 // 2048)
     assert lib.fa_decode_workspace_bytes(ctypes.byref(a)) == rows * 128 * 4 + rows * 4 + 256
+    # batch 8: 8 x 64 x 8 items of 512 keys are the first to reach 4096
+    b8 = decode_args(batch=8)
+    rows8 = 8 * 32 * (32768 // 512)
+    assert lib.fa_decode_workspace_bytes(ctypes.byref(b8)) == rows8 * 128 * 4 + rows8 * 4 + 256
     assert lib.fa_paged_decode(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE
     assert lib.fa_paged_decode(ctypes.byref(decode_args(max_seq_len=100)), 0x6000, 1 << 40,
                                None) == _lib.FA_E_INVALID

@@ -283,8 +283,20 @@ static bool use_stream(const fa_decode_args& a) {
          a.k_stride[1] < lim && a.v_stride[1] >= 0 && a.v_stride[1] < lim;
 }
 
+// Keys per split.  The streaming kernel takes the largest of kSplitMax,
+// kSplitMax / 2, .. kSplitMin whose item count (estimated from max_seq_len)
+// gives every resident wave at least kDecItemsPerWave items.
 static int decode_split_size(const fa_decode_args& a) {
-  return use_stream(a) ? DecStream::kSplit : dec_chunk(a.head_dim);
+  if (!use_stream(a)) return dec_chunk(a.head_dim);
+  const int G = a.num_heads / a.num_kv_heads;
+  const int64_t heads = (int64_t)a.num_kv_heads * (G / decode_group_size(a));
+  const int64_t waves = (int64_t)device_cu_count() * DecStream::kWavesPerCU;
+  int s = DecStream::kSplitMax;
+  for (; s > DecStream::kSplitMin; s /= 2) {
+    const int64_t items = (int64_t)a.batch * ((a.max_seq_len + s - 1) / s) * heads;
+    if (items >= tiles::kDecItemsPerWave * waves) break;
+  }
+  return s;
 }
 
 int decode_num_splits(const fa_decode_args& a) {
@@ -331,7 +343,7 @@ static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
             1, std::min<int64_t>((items + DecStream::kWavesPerWG - 1) / DecStream::kWavesPerWG,
                                  (int64_t)device_cu_count() * DecStream::kWavesPerCU /
                                      DecStream::kWavesPerWG));
-        DecodeWsS wss{ws.po, ws.plse, ws.nsplit};
+        DecodeWsS wss{ws.po, ws.plse, ws.nsplit, ws.split};
         hipLaunchKernelGGL((decode_stream_kernel<T, GB>), dim3((unsigned)wgs),
                            dim3(64 * DecStream::kWavesPerWG), 0,
                            st, a, wss);

@@ -28,8 +28,9 @@
 //    first tile when the wave's query slot is free;
 //  * at the end of an item each lane writes its 32 normalised O^T values and
 //    the head's base-2 LSE for the combine kernel.
-// A sequence's item count is ceil(len / kSplit) * heads / GB; the first wave
+// A sequence's item count is ceil(len / split) * heads / GB; the first wave
 // prefix-sums these over the batch into LDS, so the grid never holds empty work.
+// split (keys per item) is chosen per call by the launcher from the sizes.
 #pragma once
 
 #include "fa355.h"
@@ -39,7 +40,8 @@ namespace fa {
 
 struct DecStream {
   static constexpr int D = 128;
-  static constexpr int kSplit = tiles::kDecSplitKeys;      // keys per item / partial
+  static constexpr int kSplitMax = tiles::kDecSplitKeysMax;  // keys per item, largest choice
+  static constexpr int kSplitMin = tiles::kDecSplitKeysMin;  // smallest choice
   static constexpr int kTile = tiles::kDecTileKeys;        // keys per tile
   static constexpr int kDepth = tiles::kDecTilesInFlight;  // tiles in the per-wave LDS ring
   static constexpr int kMaxBatch = 1024;
@@ -54,6 +56,7 @@ struct DecodeWsS {
   float* po;    // [B, Hq, nsplit, D]
   float* plse;  // [B, Hq, nsplit]
   int nsplit;
+  int split;    // keys per item (a multiple of kTile)
 };
 
 // Item -> (b, kv head, head group, split, key range) through the batch
@@ -72,7 +75,7 @@ __device__ __forceinline__ const_i32_ptr as_const(const int32_t* p) {
 }
 
 __device__ __forceinline__ DecItem dec_item(int I, const int* pfx, const_i32_ptr seq_lens, int cap,
-                                            int B, int HG, int ngroups) {
+                                            int B, int HG, int ngroups, int split) {
   const int u = I / HG, h = I - u * HG;  // unit (sequence, split), head slot
   int lo = 0, hi = B;  // largest b with pfx[b] <= u
   while (hi - lo > 1) {
@@ -87,8 +90,8 @@ __device__ __forceinline__ DecItem dec_item(int I, const int* pfx, const_i32_ptr
   it.c = u - __builtin_amdgcn_readfirstlane(pfx[it.b]);
   it.hk = h / ngroups;
   it.hg = h % ngroups;
-  it.n_begin = it.c * DecStream::kSplit;
-  it.n_end = min(it.n_begin + DecStream::kSplit, len);
+  it.n_begin = it.c * split;
+  it.n_end = min(it.n_begin + split, len);
   it.ntiles = (it.n_end - it.n_begin + DecStream::kTile - 1) / DecStream::kTile;
   return it;
 }
@@ -177,6 +180,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   const int ngroups = G / GB;
   const int HG = a.num_kv_heads * ngroups;
   const int cap = a.max_blocks * a.page_size;
+  const int split = ws.split;
   const const_i32_ptr seq_lens = as_const(a.seq_lens);
 
   // ---- batch prefix sums of split counts (first wave)
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
       int cnt = 0;
       if (b < B) {
         const int len = max(0, min(a.seq_lens[b], cap));
-        cnt = (len + S::kSplit - 1) / S::kSplit;
+        cnt = (len + split - 1) / split;
       }
       int incl = cnt;
 #pragma unroll
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   // tile), which the fixed vmcnt in lds_read_tile relies on.  The page index
   // of a tile is read (scalar load) one prepare() early.
   int pI = I0, pt = 0;
-  DecItem pit = dec_item(pI, pfx, seq_lens, cap, B, HG, ngroups);
+  DecItem pit = dec_item(pI, pfx, seq_lens, cap, B, HG, ngroups, split);
   bool pdone = false;
   auto page_of = [&](const DecItem& it, int t) -> int {
     const_i32_ptr bt = as_const(a.block_table) + (int64_t)it.b * a.block_table_stride;
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
       ++pt;
     } else if (pI + W < I1) {
       pt = 0;
-      pit = dec_item(pI += W, pfx, seq_lens, cap, B, HG, ngroups);
+      pit = dec_item(pI += W, pfx, seq_lens, cap, B, HG, ngroups, split);
     } else {
       pdone = true;  // stays on the last tile
       return;
@@ -339,7 +343,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   // (l16, grp) holds S^T[key 4 grp + i][head l16] and O^T[16 db + 4 grp + i]
   // [head l16]; ms / lsum belong to head l16.
   int cI = I0, ct = 0;
-  DecItem cit = dec_item(cI, pfx, seq_lens, cap, B, HG, ngroups);
+  DecItem cit = dec_item(cI, pfx, seq_lens, cap, B, HG, ngroups, split);
   u32x4 qb[D / 32];
   float ms = neg_inf(), lsum = 0.f;
   f32x4 o[D / 16];
@@ -424,7 +428,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
     if (++ct == cit.ntiles) {
       finish_item();
       ct = 0;
-      if ((cI += W) < I1) cit = dec_item(cI, pfx, seq_lens, cap, B, HG, ngroups);
+      if ((cI += W) < I1) cit = dec_item(cI, pfx, seq_lens, cap, B, HG, ngroups, split);
     }
   };
 

@@ -70,11 +70,20 @@ constexpr int kBwd64QueryRows = 64;
 constexpr int kBwdPreRows = 4;
 
 // ---- decode, head_dim 128 (fa_decode_stream.h)
-// Persistent waves; work item = 512-key split x one KV head x its query heads
-// (up to 8, the 16x16x32 MFMA columns); 16-key tiles, two in flight per wave.
-// Evidence: T2 (32k context) reads 1.006x its algorithmic bytes
-// (FETCH_SIZE) at 73% of 8 TB/s.
-constexpr int kDecSplitKeys = 512;
+// Persistent waves; work item = a split of keys x one KV head x its query
+// heads (up to 8, the 16x16x32 MFMA columns); 16-key tiles, two in flight
+// per wave.  Keys per split: the largest of kDecSplitKeysMax, /2, /4 ..
+// kDecSplitKeysMin whose item count, estimated from max_seq_len, is at least
+// kDecItemsPerWave per resident wave (long items amortise each item's query
+// load and partial-result store; enough items keep every wave streaming).
+// Evidence (C4 = 64 sequences of 1083-32645 keys, T2 = 64 x 32768; % of
+// 8 TB/s, cache flushed by a read): split 256: 67.6 / 66.8; 512: 71.3 /
+// 74.1; 1024: 75.3 / 76.3; 2048: 79.5 / 80.9; 4096: 66.2 / 83.4 (C4 then
+// has ~1 item per wave, and max_seq_len cannot tell it from T2).  T2 reads
+// 1.006x its algorithmic bytes (FETCH_SIZE).
+constexpr int kDecSplitKeysMax = 2048;
+constexpr int kDecSplitKeysMin = 512;
+constexpr int kDecItemsPerWave = 2;
 constexpr int kDecTileKeys = 16;
 constexpr int kDecTilesInFlight = 2;
 
