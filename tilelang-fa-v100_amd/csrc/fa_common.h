@@ -204,6 +204,11 @@ __device__ __forceinline__ float wave_sum(float x) {
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
   return x;
 }
+__device__ __forceinline__ int wave_sum_int(int x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
 
 // Epilogue of the forward cores for one valid row: the lane holds
 // o[dt][4g + i] = O[row][col0 + 32dt + 8g + 4lh + i] (unnormalised) and the row's

@@ -45,7 +45,8 @@ struct DecodeWs {
   float* po;    // [B, Hq, nsplit, D]   normalised partial outputs
   float* plse;  // [B, Hq, nsplit]      base-2 log-sum-exp of each chunk
   int nsplit;
-  int split;    // keys per split
+  int split;       // keys per split
+  int* split_dev;  // when set, the split size used is read here (the streaming kernel's)
 };
 
 template <class T, int D, int GB>
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(fa_decode_args a,
 template <class T, int D>
 __global__ __launch_bounds__(64) void decode_combine_kernel(fa_decode_args a,
                                                             DecodeWs ws) {
-  const int CH = ws.split;
+  const int CH = ws.split_dev ? *ws.split_dev : ws.split;
   constexpr int NP = (D + 127) / 128;  // d pairs per lane: 2*lane + 128*k
   __shared__ float wts[64];
   const int hq = blockIdx.x % a.num_heads;
@@ -343,7 +344,7 @@ static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
             1, std::min<int64_t>((items + DecStream::kWavesPerWG - 1) / DecStream::kWavesPerWG,
                                  (int64_t)device_cu_count() * DecStream::kWavesPerCU /
                                      DecStream::kWavesPerWG));
-        DecodeWsS wss{ws.po, ws.plse, ws.nsplit, ws.split};
+        DecodeWsS wss{ws.po, ws.plse, ws.split_dev, ws.nsplit, ws.split};
         hipLaunchKernelGGL((decode_stream_kernel<T, GB>), dim3((unsigned)wgs),
                            dim3(64 * DecStream::kWavesPerWG), 0,
                            st, a, wss);
@@ -352,11 +353,15 @@ static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
         return launch_combine<T, D>(a, ws, st);
       }
     }
+    ws.split_dev = nullptr;  // the chunked kernel uses the launcher's split
     hipLaunchKernelGGL((decode_split_kernel<T, D, GB>), dim3((unsigned)items), dim3(256), 0, st,
                        a, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    return launch_combine<T, D>(a, ws, st);
   }
+  // No split kernel ran, so no split size was recorded on the device.
+  ws.split_dev = nullptr;
   return launch_combine<T, D>(a, ws, st);
 }
 
@@ -389,6 +394,8 @@ hipError_t launch_decode(const fa_decode_args& a, void* workspace, hipStream_t s
   char* base = static_cast<char*>(workspace);
   ws.po = reinterpret_cast<float*>(base);
   ws.plse = reinterpret_cast<float*>(base + rows * a.head_dim * sizeof(float));
+  // One int after the partial LSEs (inside the workspace's 256-byte tail).
+  ws.split_dev = reinterpret_cast<int*>(ws.plse + rows);
   return a.dtype == FA_DTYPE_BF16 ? launch_decode_t<BFloat16>(a, ws, st)
                                   : launch_decode_t<Half>(a, ws, st);
 }

@@ -30,7 +30,10 @@
 //    the head's base-2 LSE for the combine kernel.
 // A sequence's item count is ceil(len / split) * heads / GB; the first wave
 // prefix-sums these over the batch into LDS, so the grid never holds empty work.
-// split (keys per item) is chosen per call by the launcher from the sizes.
+// split (keys per item) is chosen per call by the launcher from the sizes
+// (max_seq_len); the first wave doubles it when the actual lengths still give
+// every wave kDecItemsPerWave items at twice the split, and workgroup 0
+// records the split it used for the combine kernel.
 #pragma once
 
 #include "fa355.h"
@@ -55,8 +58,9 @@ struct DecStream {
 struct DecodeWsS {
   float* po;    // [B, Hq, nsplit, D]
   float* plse;  // [B, Hq, nsplit]
-  int nsplit;
-  int split;    // keys per item (a multiple of kTile)
+  int* split_out;  // the split size used (written by workgroup 0)
+  int nsplit;      // partials per (sequence, head) the workspace holds at `split`
+  int split;       // keys per item chosen by the launcher (a multiple of kTile)
 };
 
 // Item -> (b, kv head, head group, split, key range) through the batch
@@ -180,11 +184,23 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   const int ngroups = G / GB;
   const int HG = a.num_kv_heads * ngroups;
   const int cap = a.max_blocks * a.page_size;
-  const int split = ws.split;
   const const_i32_ptr seq_lens = as_const(a.seq_lens);
 
-  // ---- batch prefix sums of split counts (first wave)
+  // ---- split size, then batch prefix sums of split counts (first wave)
+  __shared__ int split_sh;
   if (wv == 0) {
+    int split = ws.split;
+    int units2 = 0;  // items per head slot at twice the split
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      const int b = b0 + lane;
+      const int len = b < B ? max(0, min(a.seq_lens[b], cap)) : 0;
+      units2 += wave_sum_int((len + 2 * split - 1) / (2 * split));
+    }
+    if ((int64_t)units2 * HG >= (int64_t)tiles::kDecItemsPerWave * gridDim.x * W) split *= 2;
+    if (lane == 0) {
+      split_sh = split;
+      if (blockIdx.x == 0) *ws.split_out = split;
+    }
     int base = 0;
     for (int b0 = 0; b0 < B; b0 += 64) {
       const int b = b0 + lane;
@@ -205,6 +221,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
     if (lane == 0) pfx[0] = 0;
   }
   __syncthreads();
+  const int split = __builtin_amdgcn_readfirstlane(split_sh);
   // Items are numbered unit-major, head-slot-minor.  A workgroup owns a
   // contiguous range of them (a multiple of W long) and wave wv takes every
   // W-th one from offset wv, so at any time the waves of a workgroup work on
