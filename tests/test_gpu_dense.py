@@ -24,6 +24,8 @@ FWD_CASES = [
     (1, 1000, 257, 2, 2, 64, True, torch.float16),       # Sq > Sk: empty rows
     (1, 256, 256, 4, 4, 256, False, torch.float16),      # D = 256
     (1, 129, 129, 2, 2, 256, True, torch.bfloat16),
+    (1, 7, 5, 2, 1, 256, False, torch.float16),          # D = 256: one partial tile each way
+    (2, 40, 1003, 4, 2, 256, True, torch.float16),       # D = 256: Sk > Sq, GQA, ragged keys
     (3, 64, 64, 8, 8, 128, False, torch.float16),
     (1, 1, 77, 4, 1, 128, True, torch.float16),          # single query row, MQA
     (1, 1024, 1024, 16, 16, 128, True, torch.float16),   # reference test_compare_ref row
