@@ -42,6 +42,8 @@ def rows_ready(t: torch.Tensor) -> torch.Tensor:
     contiguous, every other stride a multiple of 8 elements and the base
     16-byte aligned.
     """
+    if t.is_contiguous() and t.data_ptr() % 16 == 0 and t.shape[-1] % 8 == 0:
+        return t  # common case: every stride is a multiple of the last dim
     ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
     if ok:
         for size, st in zip(t.shape[:-1], t.stride()[:-1]):
@@ -53,7 +55,8 @@ def rows_ready(t: torch.Tensor) -> torch.Tensor:
 
 def strides(t: torch.Tensor, n: int) -> tuple:
     """Element strides of the leading n dimensions (0 for size-1 dims)."""
-    return tuple(0 if t.shape[i] == 1 else t.stride(i) for i in range(n))
+    sh, st = t.shape, t.stride()
+    return tuple(0 if sh[i] == 1 else st[i] for i in range(n))
 
 
 def as_int32(t: torch.Tensor, device: torch.device, name: str) -> torch.Tensor:

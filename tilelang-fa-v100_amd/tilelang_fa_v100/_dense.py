@@ -46,9 +46,10 @@ def window_bounds(window_size) -> tuple:
     return left, right
 
 
-def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1)):
-    """Returns (out [B,Sq,H,D], lse [B,H,Sq] fp32)."""
-    B, Sq, Sk, H, Hk, D = check_shapes(q, k, v)
+def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1), shapes=None):
+    """Returns (out [B,Sq,H,D], lse [B,H,Sq] fp32).  shapes: check_shapes' result
+    when the caller has already validated q, k, v."""
+    B, Sq, Sk, H, Hk, D = shapes if shapes is not None else check_shapes(q, k, v)
     q, k, v = rows_ready(q), rows_ready(k), rows_ready(v)
     # K / V sequence strides must stay below 2^24 elements (fa_fwd).
     k = k.contiguous() if k.stride(1) >= 1 << 24 else k
@@ -69,8 +70,7 @@ def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1)):
     a.has_window = int(tuple(window) != (-1, -1))
     a.window_left, a.window_right = window
     lib = _lib.load()
-    with torch.cuda.device(q.device):
-        _lib.check(lib.fa_fwd(ctypes.byref(a), _lib.stream_handle(q.device)), "fa_fwd")
+    _lib.check(_lib.call_on(q.device, lambda st: lib.fa_fwd(ctypes.byref(a), st)), "fa_fwd")
     return out, lse
 
 
@@ -112,7 +112,6 @@ def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
     if nbytes == 0:
         _lib.check(_lib.FA_E_INVALID, "fa_bwd_workspace_bytes")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
-        _lib.check(lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), nbytes,
-                              _lib.stream_handle(q.device)), "fa_bwd")
+    _lib.check(_lib.call_on(q.device, lambda st: lib.fa_bwd(ctypes.byref(a), ws.data_ptr(),
+                                                            nbytes, st)), "fa_bwd")
     return dq, dk, dv

@@ -172,3 +172,16 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def call_on(device: torch.device, fn):
+    """Runs fn(stream) with `device` current and its current stream.
+
+    The library launches on the stream it is given and reads the current
+    device (CU count); when `device` is already current the device guard
+    (a few microseconds per call) is skipped.
+    """
+    if device.index == torch.cuda.current_device():
+        return fn(torch.cuda.current_stream().cuda_stream)
+    with torch.cuda.device(device):
+        return fn(torch.cuda.current_stream(device).cuda_stream)

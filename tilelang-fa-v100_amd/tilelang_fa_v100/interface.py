@@ -44,13 +44,13 @@ class FlashAttnTileLangVFunc(torch.autograd.Function):
         for name, t in (("q", q), ("k", k), ("v", v)):
             require_half(t, name)
         require_same({"q": q, "k": k, "v": v}, "dtype")
-        _dense.check_shapes(q, k, v)
+        shapes = _dense.check_shapes(q, k, v)
         for name, t in (("q", q), ("k", k), ("v", v)):
             require_cuda(t, name)
         require_same({"q": q, "k": k, "v": v}, "device")
         scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
         window = _dense.window_bounds(window_size)
-        out, lse = _dense.forward(q, k, v, scale, causal, window)
+        out, lse = _dense.forward(q, k, v, scale, causal, window, shapes=shapes)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.causal = bool(causal)
         ctx.window = window
