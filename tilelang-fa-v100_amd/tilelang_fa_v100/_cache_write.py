@@ -74,6 +74,5 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping):
     a.page_size, a.num_pages = page_size, num_pages
     a.dtype = _lib.dtype_code(key.dtype)
     lib = _lib.load()
-    with torch.cuda.device(dev):
-        _lib.check(lib.fa_reshape_and_cache(ctypes.byref(a), _lib.stream_handle(dev)),
-                   "fa_reshape_and_cache")
+    _lib.check(_lib.call_on(dev, lambda st: lib.fa_reshape_and_cache(ctypes.byref(a), st)),
+               "fa_reshape_and_cache")

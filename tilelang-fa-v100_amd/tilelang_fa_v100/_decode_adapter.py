@@ -90,12 +90,16 @@ def decode_forward(q, k_cache, v_cache, block_table, seq_lens,
     a, out, lse, keep = _decode_args(q, k_cache, v_cache, block_table, seq_lens, block_size,
                                      num_kv_heads, softmax_scale, return_lse)
     lib = _lib.load()
-    nbytes = lib.fa_decode_workspace_bytes(ctypes.byref(a))
-    if nbytes == 0:
-        _lib.check(_lib.FA_E_INVALID, "fa_decode_workspace_bytes")
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
-        _lib.check(lib.fa_paged_decode(ctypes.byref(a), ws.data_ptr(), nbytes,
-                                       _lib.stream_handle(q.device)), "fa_paged_decode")
+
+    def run(stream):
+        # The workspace size depends on the current device (its CU count), so
+        # it is queried with the launch's device current.
+        nbytes = lib.fa_decode_workspace_bytes(ctypes.byref(a))
+        if nbytes == 0:
+            _lib.check(_lib.FA_E_INVALID, "fa_decode_workspace_bytes")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        return lib.fa_paged_decode(ctypes.byref(a), ws.data_ptr(), nbytes, stream)
+
+    _lib.check(_lib.call_on(q.device, run), "fa_paged_decode")
     del keep
     return (out, lse) if return_lse else out

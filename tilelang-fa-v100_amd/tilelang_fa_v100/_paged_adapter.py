@@ -112,16 +112,19 @@ def paged_forward_splits(q, k_cache, v_cache, block_table, seq_lens,
     a.window_k = int(sliding_window_k)
     a.dtype = _lib.dtype_code(q.dtype)
     lib = _lib.load()
-    with torch.cuda.device(dev):
-        if num_splits is None:
-            num_splits = lib.fa_paged_prefill_num_splits(ctypes.byref(a))
-            _lib.check(min(num_splits, 0), "fa_paged_prefill_num_splits")
-        nbytes = lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), int(num_splits))
+
+    def run(stream):
+        ns = num_splits
+        if ns is None:  # chosen from the sizes and the current device's CU count
+            ns = lib.fa_paged_prefill_num_splits(ctypes.byref(a))
+            _lib.check(min(ns, 0), "fa_paged_prefill_num_splits")
+        nbytes = lib.fa_paged_prefill_splitkv_workspace_bytes(ctypes.byref(a), int(ns))
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
-        _lib.check(lib.fa_paged_prefill_splitkv(ctypes.byref(a), int(num_splits),
-                                                ws.data_ptr() if ws is not None else None,
-                                                nbytes, _lib.stream_handle(dev)),
-                   "fa_paged_prefill_splitkv")
+        return lib.fa_paged_prefill_splitkv(ctypes.byref(a), int(ns),
+                                            ws.data_ptr() if ws is not None else None,
+                                            nbytes, stream)
+
+    _lib.check(_lib.call_on(dev, run), "fa_paged_prefill_splitkv")
     if target is not out:
         out.copy_(target)
     return out, lse
