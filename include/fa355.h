@@ -197,8 +197,8 @@ int fa_paged_prefill(const fa_paged_args* args, void* stream);
  * which its configs never enable (_kernels_paged.py:353-364) and which
  * walks the splits sequentially inside one block.
  *   fa_paged_prefill_num_splits: the split count paged_forward uses for
- *     these sizes (1 = no split); reads no device data.  Negative fa_status
- *     on invalid arguments.
+ *     these sizes and the current device's CU count (1 = no split); reads
+ *     no device data.  Negative fa_status on invalid arguments.
  *   fa_paged_prefill_splitkv_workspace_bytes: bytes for num_splits
  *     (0 for num_splits == 1 or invalid arguments).
  *   fa_paged_prefill_splitkv: num_splits in [1, 64]; 1 is fa_paged_prefill
@@ -243,7 +243,10 @@ typedef struct fa_decode_args {
 } fa_decode_args;
 
 /* Replaces the decode kernel (_kernels_paged.py:393-489) driven by
- * decode_forward (_decode_adapter.py:15-47). */
+ * decode_forward (_decode_adapter.py:15-47).  The workspace size depends on
+ * the sizes and on the current device's CU count (the keys per split are
+ * chosen from both), so query it with the device current that the launch
+ * will use. */
 size_t fa_decode_workspace_bytes(const fa_decode_args* args);
 int fa_paged_decode(const fa_decode_args* args, void* workspace,
                     size_t workspace_bytes, void* stream);
