@@ -301,6 +301,24 @@ def extras(fa, dev, reps):
     res.update([flop_entry("T1_fwd", f_fwd, ms, api)])
     del q, k, v, do
 
+    # head_dim 256 at the T1 sequence length (B=2, H=8: the same bytes per row)
+    q, k, v, do = dense_inputs(2, 8192, 8, 256, torch.float16, dev)
+    for t in (q, k, v):
+        t.requires_grad_()
+    f_fwd = 4 * 256 * 8 * dense_pairs(8192, 8192, True) * 2
+
+    def t1_d256():
+        q.grad = k.grad = v.grad = None
+        o = fa.tilelang_flash_attn_func(q, k, v, causal=True)
+        o.backward(do)
+
+    ms, api = time_reps(t1_d256, max(reps // 4, 3), 1)
+    res.update([flop_entry("T1_D256_fwd_bwd", 3.5 * f_fwd, ms, api)])
+    ms, api = time_reps(lambda: fa.tilelang_flash_attn_func(q.detach(), k.detach(), v.detach(),
+                                                          causal=True), reps, 3)
+    res.update([flop_entry("T1_D256_fwd", f_fwd, ms, api)])
+    del q, k, v, do
+
     # C3: paged causal prefill fp16, 8 seqs U[512,4096], 32/8 heads, D=128
     lens, g = c3_lens()
     c = paged_inputs(lens, lens, [0] * 8, 32, 8, 128, torch.float16, dev, g)

@@ -170,6 +170,11 @@ def dtype_code(dtype: torch.dtype) -> int:
     raise TypeError(f"unsupported dtype {dtype}; expected torch.float16 or torch.bfloat16")
 
 
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of `device`'s current stream, as an integer."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def call_on(device: torch.device, fn):
     """Runs fn(stream) with `device` current and its current stream.
 
