@@ -58,10 +58,11 @@ def test_c3_config_exact():
     check(c)
 
 
-def test_c5_like_chunked_prefill_bf16():
+@pytest.mark.parametrize("D", [128, 256])
+def test_c5_like_chunked_prefill_bf16(D):
     # BASELINE configs[4] shape, fewer sequences: 512 new tokens after a prefix.
     pf = [1751, 3120, 244, 127]
-    c = make_case(1, [512] * 4, [p + 512 for p in pf], pf, 64, 8, 128, dtype=torch.bfloat16)
+    c = make_case(1, [512] * 4, [p + 512 for p in pf], pf, 64, 8, D, dtype=torch.bfloat16)
     check(c)
 
 
