@@ -139,3 +139,24 @@ def test_long_odd_length_d256():
                                                 v.repeat_interleave(2, 1), vis, 256 ** -0.5)
     assert_close(out[rows], r_out)
     assert_lse(lse.cpu()[:, rows], r_lse)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_v_cache_with_its_own_token_stride(D):
+    # V cache a column slice of a wider allocation: its token and page strides
+    # differ from K's, and the two-phase cores DMA K and V rows each with
+    # their own row stride.
+    c = make_case(9, [300, 40], [700, 40], [400, 0], 8, 2, D)
+    kc, vc = c["k_cache"], c["v_cache"]
+    wide = torch.zeros(*vc.shape[:-1], D + 64, dtype=vc.dtype)
+    wide[..., :D] = vc
+    vd = wide.to(DEV)[..., :D]
+    assert vd.stride(1) != kc.stride(1)
+    out, lse = fa.tilelang_paged_forward(
+        c["q"].to(DEV), kc.to(DEV), vd, c["block_table"].to(DEV), c["seq_lens"].to(DEV),
+        c["query_start_loc"].to(DEV), c["prefix_kv_lens"].to(DEV), block_size=c["page"],
+        num_kv_heads=2, causal=True)
+    r_out, r_lse = ref.paged_attention(c["q"], kc, vc, c["block_table"], c["seq_lens"],
+                                       c["query_start_loc"], c["prefix_kv_lens"], causal=True)
+    assert_close(out, r_out)
+    assert_lse(lse, r_lse)
