@@ -109,3 +109,15 @@ def test_long_splits_agree_with_paged_prefill(lens_kind):
     ref_out, _ = fa.tilelang_paged_forward(q, kc, vc, bt, sl, qsl, pfx, causal=True)
     assert_close(out, ref_out.view(B, 32, 128).float().cpu())
     assert rel_l2(out, ref_out.view(B, 32, 128).float().cpu()) < 1e-2
+
+
+def test_v_cache_with_its_own_token_stride():
+    q, kc, vc, bt, sl, page = make_case(12, [700, 3000, 45], 32, 8, 128)
+    wide = torch.zeros(*vc.shape[:-1], 192, dtype=vc.dtype)
+    wide[..., :128] = vc
+    vd = wide.to(DEV)[..., :128]
+    assert vd.stride(1) != kc.stride(1)
+    out = fa.tilelang_decode_forward(q.to(DEV), kc.to(DEV), vd, bt.to(DEV), sl.to(DEV),
+                                     block_size=page)
+    r_out, _ = ref.decode_attention(q, kc, vc, bt, sl)
+    assert_close(out, r_out)

@@ -87,6 +87,23 @@ def test_forward_k_and_v_with_different_row_strides(D):
     assert_close(out, r_out)
 
 
+def test_backward_k_and_v_with_different_row_strides():
+    g = torch.Generator().manual_seed(4)
+    q, k, do = randn(g, 1, 300, 4, 128), randn(g, 1, 300, 2, 128), randn(g, 1, 300, 4, 128)
+    v_wide = randn(g, 1, 300, 2, 192)
+    qd, kd = q.to(DEV).requires_grad_(), k.to(DEV).requires_grad_()
+    vw = v_wide.to(DEV).requires_grad_()
+    vd = vw[..., :128]
+    assert vd.stride(1) != kd.stride(1)
+    out = fa.tilelang_flash_attn_func(qd, kd, vd, causal=True)
+    out.backward(do.to(DEV))
+    v = v_wide[..., :128].contiguous()
+    r_dq, r_dk, r_dv = ref.dense_attention_backward(q, k, v, do, causal=True)
+    assert_close(qd.grad, r_dq, what="dq")
+    assert_close(kd.grad, r_dk, what="dk")
+    assert_close(vw.grad[..., :128], r_dv, what="dv")
+
+
 BWD_CASES = [
     (4, 2048, 2048, 16, 16, 128, True, torch.float16),
     (2, 200, 200, 4, 4, 64, False, torch.float16),
