@@ -70,3 +70,81 @@ def assert_lse(got, ref, atol=LSE_ATOL, what="lse"):
     assert torch.equal(torch.isneginf(got), torch.isneginf(ref)), f"{what}: -inf pattern differs"
     err = (got[fin] - ref[fin]).abs()
     assert err.numel() == 0 or err.max().item() <= atol, f"{what}: max err {err.max().item():.3e}"
+
+
+# ------------------------------------------------------------- needle inputs
+# Scores that make P one-hot, so the output must equal one V row bit for bit.
+# Key j carries the base-16 digits of j in dims 0..3 and q is +/-(1, 16, 256,
+# 4096) there and 0 elsewhere, so s = q . k = +/-j exactly (integer products
+# and sums below 2^24 are exact in the fp32 accumulators).  With a softmax
+# scale whose fp32 product with log2(e) rounds to exactly 128, every score
+# is a multiple of 128 in the kernels' base-2 domain: the row maximum gets
+# p = exp2(0) = 1 and every other key p <= 2^-128, which vanishes next to it.
+# Rising scores (+) put the needle on the LAST visible key of a row (causal
+# edge, seq_len boundary, right window edge); falling scores (-) on the FIRST
+# (left window edge, key 0).  An off-by-one in a mask or a wrong page then
+# returns another V row, which equality detects.
+
+NEEDLE_DIGITS = (1.0, 16.0, 256.0, 4096.0)
+
+
+def needle_scale() -> float:
+    """A float32 scale with fl32(scale * fl32(log2 e)) == 128 exactly."""
+    import numpy as np
+
+    log2e = np.float32(1.4426950408889634)
+    x = np.float32(128.0) / log2e
+    for _ in range(64):
+        p = np.float32(x * log2e)
+        if p == np.float32(128.0):
+            return float(x)
+        x = np.nextafter(x, np.float32(np.inf) if p < 128 else np.float32(-np.inf),
+                         dtype=np.float32)
+    raise AssertionError("no float32 scale maps to 128")
+
+
+def needle_keys(gen, n, heads, D, dtype=torch.float16):
+    """K [n, heads, D]: digits of the key index in dims 0..3, N(0,1) elsewhere."""
+    assert n <= 1 << 16
+    k = torch.randn(n, heads, D, generator=gen)
+    j = torch.arange(n)
+    for d in range(4):
+        k[:, :, d] = ((j >> (4 * d)) & 15).float().unsqueeze(1)
+    return k.to(dtype)
+
+
+def needle_query(rows, heads, D, sign=1, dtype=torch.float16):
+    """q [rows, heads, D] = sign * (1, 16, 256, 4096, 0, ...)."""
+    q = torch.zeros(rows, heads, D)
+    q[:, :, :4] = torch.tensor(NEEDLE_DIGITS) * sign
+    return q.to(dtype)
+
+
+def needle_expected(v_rows, visible, sign):
+    """Per query row the V row of its last (sign > 0) or first visible key.
+
+    v_rows [n, H, D] (already in query-head order), visible [Sq, n] bool.
+    Rows with no visible key expect zeros.  Returns [Sq, H, D].
+    """
+    Sq, n = visible.shape
+    if n == 0 or Sq == 0:
+        return torch.zeros(Sq, *v_rows.shape[1:], dtype=v_rows.dtype)
+    idx = torch.arange(n).expand(Sq, n)
+    if sign > 0:
+        pick = torch.where(visible, idx, torch.full_like(idx, -1)).max(1).values
+    else:
+        pick = torch.where(visible, idx, torch.full_like(idx, n)).min(1).values
+    out = torch.zeros(Sq, *v_rows.shape[1:], dtype=v_rows.dtype)
+    ok = visible.any(1)
+    out[ok] = v_rows[pick[ok]]
+    return out
+
+
+def assert_equal_rows(got, want, what="out"):
+    """Bit-exact equality; on failure names the first differing row."""
+    got = got.cpu()
+    want = want.to(got.dtype).cpu()
+    same = (got == want) | (torch.isnan(got) & torch.isnan(want))
+    if not bool(same.all()):
+        bad = (~same).reshape(same.shape[0], -1).any(1).nonzero().flatten()
+        raise AssertionError(f"{what}: {bad.numel()} rows differ; first rows {bad[:8].tolist()}")

@@ -215,8 +215,8 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
     const uint16_t* orow = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
                            h * a.do_stride[2] + (int64_t)i0 * a.do_stride[1];
     const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
-    const u32x4 rq = rsrc_words(qrow, nrows * (uint32_t)a.q_stride[1] * 2u);
-    const u32x4 ro = rsrc_words(orow, nrows * (uint32_t)a.do_stride[1] * 2u);
+    const u32x4 rq = rsrc_words(qrow, span_bytes(nrows, a.q_stride[1], D));
+    const u32x4 ro = rsrc_words(orow, span_bytes(nrows, a.do_stride[1], D));
     // Opaque DMA: the loop's wait_vmem + barrier is the only wait the tile
     // needs (the compiler would otherwise wait for it, and for the dQ
     // atomics, before each dSᵀ access).

@@ -304,6 +304,14 @@ __device__ __forceinline__ void buffer_lds4(rsrc_t r, uint32_t voff, void* lds_b
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       r, (__attribute__((address_space(3))) void*)lds_block, 4, voff, 0, 0, 0);
 }
+// Bytes from the first of n rows (16-bit elements, `stride` elements apart)
+// to the end of the last row's first `width` elements: the range of a buffer
+// resource over those rows.  Rows past the n-th start at or beyond it when
+// stride >= width; a size-1 dimension may carry stride 0, and then the range
+// is still one row long.
+__device__ __forceinline__ uint32_t span_bytes(int n, int64_t stride, int width) {
+  return n > 0 ? 2u * ((uint32_t)(n - 1) * (uint32_t)stride + (uint32_t)width) : 0u;
+}
 // Buffer descriptor words for the inline-assembly DMA below (same fields as
 // make_rsrc: raw buffer, stride 0, num_records = bytes).
 __device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {

@@ -449,8 +449,9 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     const int nvalid = min(16, wg_hi - nw);  // n0 < wg_hi, so n0's row resolves
     const int nb = nvalid > 0 ? nw : n0;
     const uint16_t* base = kV ? P.v_ptr(nb) : P.k_ptr(nb);
-    const uint32_t bytes =
-        (uint32_t)max(nvalid, 0) * (uint32_t)(kV ? P.v_row_stride() : P.k_row_stride()) * 2u;
+    // The range ends after the last valid row's D columns (not nvalid whole
+    // strides): a size-1 sequence dimension may come with stride 0.
+    const uint32_t bytes = span_bytes(nvalid, kV ? P.v_row_stride() : P.k_row_stride(), D);
     u32x4 rs = rsrc_words(base, bytes);
     // Uniform by construction (the block-table read of a paged problem is
     // not known to be); the resource must sit in scalar registers.

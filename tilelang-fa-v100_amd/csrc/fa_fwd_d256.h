@@ -194,8 +194,9 @@ __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, floa
     const int nvalid = min(8, wg_hi - nw);  // n0 < wg_hi, so n0's row resolves
     const int nb = nvalid > 0 ? nw : n0;
     const uint16_t* base = kV ? P.v_ptr(nb) + vcol : P.k_ptr(nb);
+    // K rows are read whole, V rows one pass's DO columns from vcol.
     const uint32_t bytes =
-        (uint32_t)max(nvalid, 0) * (uint32_t)(kV ? P.v_row_stride() : P.k_row_stride()) * 2u;
+        span_bytes(nvalid, kV ? P.v_row_stride() : P.k_row_stride(), kV ? DO : D);
     u32x4 rs = rsrc_words(base, bytes);
 #pragma unroll
     for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(rs[w]);

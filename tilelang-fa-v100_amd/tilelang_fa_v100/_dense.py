@@ -46,18 +46,22 @@ def window_bounds(window_size) -> tuple:
     return left, right
 
 
-def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1), shapes=None):
+def forward(q, k, v, softmax_scale: float, causal: bool, window=(-1, -1), shapes=None,
+            with_lse: bool = True):
     """Returns (out [B,Sq,H,D], lse [B,H,Sq] fp32).  shapes: check_shapes' result
-    when the caller has already validated q, k, v."""
+    when the caller has already validated q, k, v.  with_lse=False passes no LSE
+    buffer (the kernel skips its store) and returns (out, None): the reference's
+    LSE-less tilelang_forward (_kernels_forward.py:9-91,180-185)."""
     B, Sq, Sk, H, Hk, D = shapes if shapes is not None else check_shapes(q, k, v)
     q, k, v = rows_ready(q), rows_ready(k), rows_ready(v)
     # K / V sequence strides must stay below 2^24 elements (fa_fwd).
     k = k.contiguous() if k.stride(1) >= 1 << 24 else k
     v = v.contiguous() if v.stride(1) >= 1 << 24 else v
     out = torch.empty((B, Sq, H, D), dtype=q.dtype, device=q.device)
-    lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+    lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device) if with_lse else None
     a = _lib.FwdArgs()
-    a.q, a.k, a.v, a.out, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    a.lse = lse.data_ptr() if with_lse else None
     a.q_stride[:] = strides(q, 3)
     a.k_stride[:] = strides(k, 3)
     a.v_stride[:] = strides(v, 3)

@@ -50,7 +50,12 @@ class FlashAttnTileLangVFunc(torch.autograd.Function):
         require_same({"q": q, "k": k, "v": v}, "device")
         scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
         window = _dense.window_bounds(window_size)
-        out, lse = _dense.forward(q, k, v, scale, causal, window, shapes=shapes)
+        # Without gradients and without a requested LSE (inference) the kernel
+        # skips the LSE store, as the reference's tilelang_forward does
+        # (_kernels_forward.py:176-185).
+        with_lse = bool(return_softmax) or any(ctx.needs_input_grad[:3])
+        out, lse = _dense.forward(q, k, v, scale, causal, window, shapes=shapes,
+                                  with_lse=with_lse)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.causal = bool(causal)
         ctx.window = window
