@@ -262,6 +262,15 @@ def headline(fa, steps, warmup, dev):
         _lib.check(lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), nbytes, stream), "fa_bwd")
 
     bwd_ms, bwd_api = time_reps(bwd, max(steps, 20), 3)
+    # The same launch with deterministic=1 (query-stationary dQ, no atomics).
+    a_det = _dense.bwd_args(qd, kd, vd, out, do, lse, dq, dk, dv, D ** -0.5, True, True)
+    nb_det = lib.fa_bwd_workspace_bytes(ctypes.byref(a_det))
+    ws_det = torch.empty(nb_det, dtype=torch.uint8, device=dev)
+
+    def bwd_det():
+        _lib.check(lib.fa_bwd(ctypes.byref(a_det), ws_det.data_ptr(), nb_det, stream), "fa_bwd")
+
+    det_ms, det_api = time_reps(bwd_det, max(steps, 20), 3)
     fwd_ms, fwd_api = time_reps(lambda: _dense.forward(qd, kd, vd, D ** -0.5, True),
                                 max(steps, 20), 3)
     bwd_tf = 2.5 * f_fwd / (bwd_ms * 1e-3) / 1e12
@@ -271,7 +280,8 @@ def headline(fa, steps, warmup, dev):
                 "kernel": "fa_bwd (bwd_pre + bwd_main + bwd_dq_convert)",
                 "launch_ms": round(bwd_ms, 4), "algorithmic_gflop": round(2.5 * f_fwd / 1e9, 2)}
     parts = dict([flop_entry("C2_fwd", f_fwd, fwd_ms, fwd_api),
-                  flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms, bwd_api)])
+                  flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms, bwd_api),
+                  flop_entry("C2_bwd_deterministic", 2.5 * f_fwd, det_ms, det_api)])
     return ms, f_step, roofline, parts
 
 
@@ -296,6 +306,14 @@ def extras(fa, dev, reps):
 
     ms, api = time_reps(t1, max(reps // 2, 5), 2)
     res.update([flop_entry("T1_fwd_bwd", 3.5 * f_fwd, ms, api)])
+
+    def t1_det():
+        q.grad = k.grad = v.grad = None
+        o = fa.tilelang_flash_attn_func(q, k, v, causal=True, deterministic=True)
+        o.backward(do)
+
+    ms, api = time_reps(t1_det, max(reps // 2, 5), 2)
+    res.update([flop_entry("T1_fwd_bwd_deterministic", 3.5 * f_fwd, ms, api)])
     ms, api = time_reps(lambda: fa.tilelang_flash_attn_func(q.detach(), k.detach(), v.detach(),
                                                           causal=True), reps, 3)
     res.update([flop_entry("T1_fwd", f_fwd, ms, api)])

@@ -271,3 +271,65 @@ def test_forward_without_lse(D, causal, dt):
     with torch.no_grad():
         out2 = fa.tilelang_flash_attn_func(qd, kd, vd, causal=causal)
     assert torch.equal(out2, out_ref_api)
+
+
+DET_CASES = [
+    # (B, Sq, Sk, H, Hk, D, causal, window, dtype)
+    (4, 2048, 2048, 16, 16, 128, True, (-1, -1), torch.float16),
+    (1, 300, 500, 4, 2, 128, True, (-1, -1), torch.bfloat16),      # Sk > Sq, GQA
+    (1, 500, 300, 2, 2, 128, True, (-1, -1), torch.float16),       # Sq > Sk: empty rows
+    (2, 333, 333, 4, 4, 128, False, (-1, -1), torch.float16),
+    (1, 700, 700, 4, 2, 128, True, (130, -1), torch.float16),      # window
+    (2, 200, 200, 4, 4, 64, False, (-1, -1), torch.float16),       # D = 64
+    (2, 130, 130, 8, 1, 64, True, (-1, -1), torch.float16),
+    (1, 300, 300, 4, 4, 256, True, (-1, -1), torch.float16),       # D = 256
+    (2, 200, 333, 4, 2, 256, False, (-1, -1), torch.bfloat16),
+    (1, 300, 400, 2, 2, 256, False, (50, 70), torch.float16),
+    (1, 1, 77, 2, 1, 128, False, (-1, -1), torch.float16),         # one query row
+    (1, 40, 1, 2, 2, 256, False, (-1, -1), torch.float16),         # one key
+]
+
+
+def _detids(c):
+    B, Sq, Sk, H, Hk, D, causal, w, dt = c
+    return (f"B{B}-{Sq}x{Sk}-H{H}/{Hk}-D{D}-{'c' if causal else 'nc'}-w{w[0]}_{w[1]}-"
+            f"{str(dt)[6:]}")
+
+
+@pytest.mark.parametrize("case", DET_CASES, ids=[_detids(c) for c in DET_CASES])
+def test_deterministic_backward_matches_oracle_and_repeats(case):
+    """deterministic=True: query-stationary dQ (no atomics); the gradients
+    match the oracle and two runs agree bit for bit, as the reference's
+    atomic-free kernels do (_kernels_backward.py:10-85,88-176)."""
+    B, Sq, Sk, H, Hk, D, causal, window, dt = case
+    g = torch.Generator().manual_seed(21)
+    q, k, v = randn(g, B, Sq, H, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt)
+    do = randn(g, B, Sq, H, D, dtype=dt)
+    grads = []
+    for _ in range(2):
+        qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+        out = fa.tilelang_flash_attn_func(qd, kd, vd, causal=causal, window_size=window,
+                                          deterministic=True)
+        out.backward(do.to(DEV))
+        grads.append((qd.grad, kd.grad, vd.grad))
+    r = ref.dense_attention_backward(q, k, v, do, causal=causal, window=window)
+    for got, got2, want, name in zip(grads[0], grads[1], r, ("dq", "dk", "dv")):
+        assert torch.equal(got, got2), f"{name} differs between two runs"
+        assert_close(got, want, what=name)
+        if want.abs().max() > 1e-4:
+            assert rel_l2(got, want) < 1e-2, name
+
+
+def test_deterministic_and_atomic_paths_agree():
+    """Both backward paths compute the same gradients (to fp32 summation
+    order): dk / dv come from the same kernel code, dq from either reduction."""
+    g = torch.Generator().manual_seed(22)
+    q, k, v, do = (randn(g, 2, 1000, 8, 128) for _ in range(4))
+    res = []
+    for det in (False, True):
+        qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+        out = fa.tilelang_flash_attn_func(qd, kd, vd, causal=True, deterministic=det)
+        out.backward(do.to(DEV))
+        res.append((qd.grad.float(), kd.grad, vd.grad))
+    assert torch.equal(res[0][1], res[1][1]) and torch.equal(res[0][2], res[1][2])
+    assert (res[0][0] - res[1][0]).abs().max().item() <= 2e-3

@@ -23,6 +23,7 @@
 //                       K^T of the workgroup stays in LDS.
 //   bwd_main_mfma_kernel  head_dim 128 / 256 variant (fa_bwd_mfma.h).
 //   bwd_dq_convert      dQ = scale * acc, cast to the input dtype.
+#include "fa_bwd_dq.h"
 #include "fa_bwd_mfma.h"
 #include "fa_common.h"
 #include "fa_internal.h"
@@ -98,9 +99,11 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 #pragma unroll
     for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
     if (q < Sq) {
-      float* z = dqacc + (row0 + q) * D + 8 * sub;
-      st16(z, u32x4{0, 0, 0, 0});
-      st16(z + 4, u32x4{0, 0, 0, 0});
+      if (dqacc) {  // atomic path: the dQ accumulator starts at zero
+        float* z = dqacc + (row0 + q) * D + 8 * sub;
+        st16(z, u32x4{0, 0, 0, 0});
+        st16(z + 4, u32x4{0, 0, 0, 0});
+      }
       if (sub == 0) {
         const float l = a.lse[row0 + q];
         float* st = stats + 2 * row0 + q;
@@ -114,8 +117,9 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 
 // ------------------------------------------------------------ main kernel
 // MODE (MaskMode): full attention, causal, or a window band from the
-// arguments.
-template <class T, int D, int MODE>
+// arguments.  DQ: also compute dQ (fp32 atomics into dqacc); without it the
+// kernel writes dK / dV only (deterministic path, dQ from bwd_dq_kernel).
+template <class T, int D, int MODE, bool DQ>
 __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqacc,
                                                        const float* stats) {
   using S = BwdShape<D>;
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     const int col8 = tid % S::CPR, grp = tid / S::CPR;
     constexpr int GPP = 256 / S::CPR;  // 4-row groups per pass
 #pragma unroll
-    for (int p = 0; p < S::BKV / (4 * GPP); ++p) {
+    for (int p = 0; p < (DQ ? S::BKV / (4 * GPP) : 0); ++p) {
       const int rbase = 4 * (grp + GPP * p);
       u32x4 rows[4];
 #pragma unroll
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
           sB[kq][w] = T::pack(dp[kq >> 1][e], dp[kq >> 1][e + 1]);
         }
 #pragma unroll
-      for (int kq = 0; kq < 2 * S::NQT; ++kq)
+      for (int kq = 0; kq < (DQ ? 2 * S::NQT : 0); ++kq)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           // halves of sB[kq][w] are entries e, e+1 = rows qrow, qrow+1
@@ -341,7 +345,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
           dv[dt] = T::mma32(ad, pB[kq], dv[dt]);
           dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
         }
-    } else {
+    } else if constexpr (DQ) {
       // Inactive waves contribute zero dS to the shared dQ product.
 #pragma unroll
       for (int q = 0; q < S::BQ; ++q) dSs[q * S::SS + 32 * wave + lr] = 0;
@@ -352,7 +356,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     // dQ[i0 + q][d] += sum_k dS[q][k] K[k][d] over this workgroup's 128 keys.
     {
       const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
-      if (any) {
+      if (DQ && any) {
         float* dqb = dqacc + ((int64_t)b * H + h) * Sq * D;  // [B, H, Sq, D]
         const int64_t qstride = D;
 #pragma unroll
@@ -442,54 +446,88 @@ __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(fa_bwd_args a,
 
 // ----------------------------------------------------------------- launchers
 
+// Workspace: the fp32 dQ accumulator [B, H, Sq, D] (atomic path only), then
+// the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot).
 size_t bwd_workspace_bytes(const fa_bwd_args& a) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
-  return rows * a.head_dim * sizeof(float) + 2 * rows * sizeof(float) + 256;
+  const size_t acc = a.deterministic ? 0 : rows * a.head_dim * sizeof(float);
+  return acc + 2 * rows * sizeof(float) + 256;
 }
 
+// Key-stationary main kernel for one mask mode; DQ selects the atomic dQ.
+template <class T, int D, bool DQ>
+static void launch_bwd_main(const fa_bwd_args& a, int mode, float* dqacc, const float* stats,
+                            hipStream_t st) {
+  if constexpr (D >= 128) {
+    constexpr int KB = D == 128 ? kBwdKB : 1;
+    using S2 = BwdShapeMfma<D, KB>;
+    const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
+    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S2::NW);
+    if (kvtiles == 0) return;  // no keys: dQ stays zero; dK / dV are empty
+    if (mode == kMaskCausal)
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal, KB, DQ>), grid, block, 0, st, a,
+                         dqacc, stats);
+    else if (mode == kMaskBand)
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand, KB, DQ>), grid, block, 0, st, a,
+                         dqacc, stats);
+    else
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone, KB, DQ>), grid, block, 0, st, a,
+                         dqacc, stats);
+  } else {
+    using S = BwdShape<D>;
+    const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
+    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
+    if (kvtiles == 0) return;
+    if (mode == kMaskCausal)
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskCausal, DQ>), grid, dim3(256), 0, st, a,
+                         dqacc, stats);
+    else if (mode == kMaskBand)
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskBand, DQ>), grid, dim3(256), 0, st, a,
+                         dqacc, stats);
+    else
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskNone, DQ>), grid, dim3(256), 0, st, a,
+                         dqacc, stats);
+  }
+}
+
+// Query-stationary dQ kernel (deterministic path).
+template <class T, int D>
+static void launch_bwd_dq(const fa_bwd_args& a, int mode, const float* stats, hipStream_t st) {
+  using S = BwdDqShape<D>;
+  const int qtiles = (a.seqlen_q + S::BM - 1) / S::BM;
+  const dim3 grid((unsigned)qtiles * a.num_heads * a.batch), block(64 * S::NW);
+  if (mode == kMaskCausal)
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskCausal>), grid, block, 0, st, a, stats);
+  else if (mode == kMaskBand)
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskBand>), grid, block, 0, st, a, stats);
+  else
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
+}
+
+// Default path: pre (statistics, zeroed accumulator), main with fp32 dQ
+// atomics, dQ convert.  Deterministic path: pre (statistics), main without
+// dQ, then the query-stationary dQ kernel, which writes dQ directly; every
+// output element is then produced by one fixed sequence of operations.
 template <class T, int D>
 static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
-  float* dqacc = static_cast<float*>(ws);
-  float* stats = dqacc + rows * D;  // [B*H][2][Sq]
+  const bool det = a.deterministic != 0;
+  float* dqacc = det ? nullptr : static_cast<float*>(ws);
+  float* stats = static_cast<float*>(ws) + (det ? 0 : rows * D);  // [B*H][2][Sq]
   const dim3 rgrid((unsigned)((a.seqlen_q + pre_rows_per_block<D>() - 1) / pre_rows_per_block<D>()),
                    (unsigned)(a.batch * a.num_heads));
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int mode = mask_mode(a);
-  if constexpr (D >= 128) {
-    constexpr int KB = D == 128 ? kBwdKB : 1;
-    using S2 = BwdShapeMfma<D, KB>;
-    const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
-    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S2::NW);
-    if (kvtiles == 0) {
-      // No keys: dQ stays zero; dK / dV are empty.
-    } else if (mode == kMaskCausal)
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal, KB>), grid, block, 0, st, a,
-                         dqacc, stats);
-    else if (mode == kMaskBand)
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand, KB>), grid, block, 0, st, a,
-                         dqacc, stats);
-    else
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone, KB>), grid, block, 0, st, a,
-                         dqacc, stats);
-  } else {
-    using S = BwdShape<D>;
-    const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
-    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
-    if (kvtiles == 0) {
-      // No keys: dQ stays zero; dK / dV are empty.
-    } else if (mode == kMaskCausal)
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskCausal>), grid, dim3(256), 0, st, a, dqacc,
-                         stats);
-    else if (mode == kMaskBand)
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskBand>), grid, dim3(256), 0, st, a, dqacc,
-                         stats);
-    else
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskNone>), grid, dim3(256), 0, st, a, dqacc,
-                         stats);
+  if (det) {
+    launch_bwd_main<T, D, false>(a, mode, nullptr, stats, st);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_bwd_dq<T, D>(a, mode, stats, st);
+    return hipGetLastError();
   }
+  launch_bwd_main<T, D, true>(a, mode, dqacc, stats, st);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((bwd_dq_convert_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc);

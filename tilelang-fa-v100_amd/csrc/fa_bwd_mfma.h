@@ -65,7 +65,10 @@ struct BwdShapeMfma {
 constexpr int kBwdKB = tiles::kBwd128KeyBlocksPerWave;
 
 // MODE (MaskMode): full attention, causal, or a window band from the arguments.
-template <class T, int D_, int MODE, int KB>
+// DQ: also compute dQ (dSᵀ through LDS, fp32 atomics into dqacc); without it
+// the kernel writes dK / dV only and dQ comes from bwd_dq_kernel
+// (fa_bwd_dq.h, the deterministic path).
+template <class T, int D_, int MODE, int KB, bool DQ>
 __global__ __launch_bounds__((64 * BwdShapeMfma<D_, KB>::NW), (BwdShapeMfma<D_, KB>::WPE))
 void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   using S = BwdShapeMfma<D_, KB>;
@@ -327,11 +330,13 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
             sB[kb][kq][w] = T::pack(dp[kb][e], dp[kb][e + 1]);
           }
         // dSᵀ row wrow + 32kb + lr; queries 8g + 4lh .. +3 = piece 2g + lh.
+        if constexpr (DQ) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int kq = g >> 1, w0 = 2 * (g & 1);
-          const u32x2 v = {sB[kb][kq][w0], sB[kb][kq][w0 + 1]};
-          st8(smem + dso + dsw_off(kb, g), v);
+          for (int g = 0; g < 4; ++g) {
+            const int kq = g >> 1, w0 = 2 * (g & 1);
+            const u32x2 v = {sB[kb][kq][w0], sB[kb][kq][w0 + 1]};
+            st8(smem + dso + dsw_off(kb, g), v);
+          }
         }
       }
       // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads, shared
@@ -354,7 +359,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
           }
         }
       sched_pipeline<2 * (D / 32), 4, 2 * KB, 2>();
-    } else {
+    } else if constexpr (DQ) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -366,6 +371,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, float* dqacc, const float* stats) {
   // tile whose dSᵀ is complete in dsb (waves 0 .. DQW-1, d tiles
   // dt = wave + DQW j).
   auto dq_step = [&](int h_rel, int it, int dso) {
+    if constexpr (!DQ) return;
     const int i0 = it * S::BQ;
     const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
     if (wave < S::DQW && any) {
