@@ -18,6 +18,7 @@
 //     of the dormant split variant, _kernels_paged.py:175-187).
 // The decode mask is `key < seq_len` (_kernels_paged.py:450-451).
 #include <algorithm>
+#include <mutex>
 
 #include "fa_common.h"
 #include "fa_decode_stream.h"
@@ -311,17 +312,21 @@ size_t decode_workspace_bytes(const fa_decode_args& a) {
   return rows * (size_t)a.head_dim * sizeof(float) + rows * sizeof(float) + 256;
 }
 
+// Queried once per device (std::call_once: entry points may run on several
+// host threads at once).
 int device_cu_count() {
-  static int cached[64] = {0};
+  constexpr int kMaxDevices = 64;
+  static std::once_flag once[kMaxDevices];
+  static int cached[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(once[dev], [dev] {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
     cached[dev] = n;
-  }
+  });
   return cached[dev];
 }
 
