@@ -257,6 +257,20 @@ size_t fa_decode_workspace_bytes(const fa_decode_args* args);
 int fa_paged_decode(const fa_decode_args* args, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Size of the static device scratch behind fa_paged_decode_noalloc. */
+#define FA_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): fa_paged_decode with its split-KV workspace taken from
+ * a static device array of FA_NOALLOC_SCRATCH_BYTES per GPU (held until the
+ * process ends) instead of a caller buffer.  Allocates nothing.  Problems
+ * whose fa_decode_workspace_bytes exceeds FA_NOALLOC_SCRATCH_BYTES are
+ * rejected with FA_E_WORKSPACE.  All calls on one GPU share its array: calls
+ * that overlap on that GPU (other streams, other host threads) race and
+ * must be serialised by the caller; calls on one stream are ordered. */
+int fa_paged_decode_noalloc(const fa_decode_args* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* KV-cache write (vLLM reshape_and_cache).                                 */
 /*   key, value   [num_tokens, num_kv_heads, head_dim] (strides {token, head}) */

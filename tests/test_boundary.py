@@ -204,6 +204,24 @@ def test_decode_workspace_and_checks():
                                None) == _lib.FA_E_UNSUPPORTED
 
 
+def test_decode_noalloc_rejects_before_launch():
+    """The allocation-free decode validates like fa_paged_decode and refuses
+    problems whose split-KV workspace exceeds its static scratch."""
+    lib = _lib.load()
+    limit = 64 << 20
+    big = decode_args(batch=256, num_heads=64)
+    assert lib.fa_decode_workspace_bytes(ctypes.byref(big)) > limit
+    assert lib.fa_paged_decode_noalloc(ctypes.byref(big), None) == _lib.FA_E_WORKSPACE
+    assert b"static buffer" in lib.fa_last_error_message()
+    assert lib.fa_paged_decode_noalloc(None, None) == _lib.FA_E_INVALID
+    assert lib.fa_paged_decode_noalloc(ctypes.byref(decode_args(page_size=3)),
+                                       None) == _lib.FA_E_UNSUPPORTED
+    assert lib.fa_paged_decode_noalloc(ctypes.byref(decode_args(max_seq_len=100)),
+                                       None) == _lib.FA_E_INVALID
+    # The C4 / T2 shapes (64 sequences, 32 / 8 heads, 32k keys) fit.
+    assert lib.fa_decode_workspace_bytes(ctypes.byref(decode_args())) <= limit
+
+
 # ------------------------------------------------------------------ Python API
 
 def _qkv(dtype=torch.float16, shape=(1, 8, 2, 64)):

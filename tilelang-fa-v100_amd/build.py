@@ -23,7 +23,8 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(REPO, "_build")
 LIB = os.path.join(HERE, "tilelang_fa_v100", "libfa355.so")
 
-SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_decode.hip", "fa_cache.hip", "fa_capi.cpp"]
+SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_decode.hip", "fa_cache.hip", "fa_scratch.hip",
+           "fa_capi.cpp"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -312,6 +312,27 @@ int fa_paged_decode(const fa_decode_args* a, void* ws, size_t ws_bytes, void* st
                     "fa_paged_decode launch");
 }
 
+// Same validation and kernels as fa_paged_decode; the workspace is the
+// device's static scratch array (no allocation, no workspace argument).
+int fa_paged_decode_noalloc(const fa_decode_args* a, void* stream) {
+  const int st = check_decode(a);
+  if (st != FA_OK) return st;
+  if (a->batch == 0) return ok();
+  if (a->num_pages == 0) return fail(FA_E_INVALID, "fa_paged_decode_noalloc: empty KV cache");
+  const size_t need = fa::decode_workspace_bytes(*a);
+  if (need > (size_t)FA_NOALLOC_SCRATCH_BYTES)
+    return fail(FA_E_WORKSPACE,
+                "fa_paged_decode_noalloc: this problem needs %zu bytes of split-KV scratch, "
+                "above the %zu-byte static buffer; call fa_paged_decode with a workspace",
+                need, (size_t)FA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const hipError_t e = fa::noalloc_scratch(&ws);
+  if (e != hipSuccess || !ws) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                "fa_paged_decode_noalloc scratch lookup");
+  return hip_status(fa::launch_decode(*a, ws, static_cast<hipStream_t>(stream)),
+                    "fa_paged_decode_noalloc launch");
+}
+
 // ------------------------------------------------------------------ cache write
 
 static int check_cache_write(const fa_cache_write_args* a) {

@@ -32,6 +32,11 @@ int decode_num_splits(const fa_decode_args& a);
 size_t decode_workspace_bytes(const fa_decode_args& a);
 hipError_t launch_decode(const fa_decode_args& a, void* ws, hipStream_t st);
 
+// Device address of the current device's FA_NOALLOC_SCRATCH_BYTES-byte
+// static scratch array (fa_scratch.hip), looked up on the first call per
+// device.
+hipError_t noalloc_scratch(void** ptr);
+
 hipError_t launch_cache_write(const fa_cache_write_args& a, hipStream_t st);
 
 }  // namespace fa

@@ -120,6 +120,7 @@ _PROTOTYPES = {
                                                 ctypes.c_size_t, _vp]),
     "fa_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "fa_paged_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
+    "fa_paged_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
     "fa_reshape_and_cache": (ctypes.c_int, [ctypes.POINTER(CacheWriteArgs), _vp]),
 }
 
