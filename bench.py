@@ -384,6 +384,18 @@ def extras(fa, dev, reps):
         ms, api = time_reps(run, reps, 3, flush)
         res.update([bytes_entry(name, decode_bytes(lens, 32, 8, 128), ms, api)])
         del c, qd
+
+    # Decode at the other head dims (64 sequences, 32 / 8 heads, fp16).
+    for name, D, n in (("decode_D64_64x16k", 64, 16384), ("decode_D256_64x8k", 256, 8192)):
+        lens = [n] * 64
+        c = paged_inputs([1] * 64, lens, [0] * 64, 32, 8, D, torch.float16, dev,
+                         torch.Generator().manual_seed(0), device_values=True)
+        qd = c["q"].view(64, 32, D)
+        run = lambda: fa.tilelang_decode_forward(qd, c["k_cache"], c["v_cache"],  # noqa: E731
+                                                 c["block_table"], c["seq_lens"])
+        ms, api = time_reps(run, reps, 3, flush)
+        res.update([bytes_entry(name, decode_bytes(lens, 32, 8, D), ms, api)])
+        del c, qd
     return res
 
 

@@ -274,15 +274,25 @@ int decode_group_size(const fa_decode_args& a) {
   return 1;
 }
 
-// The streaming kernel (fa_decode_stream.h) covers head_dim 128 with pages of
-// at least 16 keys, at most kMaxGroup query heads per item, and token strides
-// whose 16-row offsets fit its 32-bit lane offsets; other shapes use
-// decode_split_kernel.
+// The streaming kernel (fa_decode_stream.h) covers head_dim 64 / 128 / 256
+// with pages of at least 16 keys, at most kMaxGroup query heads per item and
+// token strides whose 16-row offsets fit its 32-bit lane offsets; other
+// shapes use decode_split_kernel.  (At head_dim 512 one tile's operands and
+// the 32 output blocks exceed a wave's registers: 289 spilled.)
 static bool use_stream(const fa_decode_args& a) {
   const int64_t lim = int64_t(1) << 26;
-  return a.head_dim == 128 && a.page_size >= 16 && a.batch <= DecStream::kMaxBatch &&
-         decode_group_size(a) <= DecStream::kMaxGroup && a.k_stride[1] >= 0 &&
+  return a.head_dim <= 256 && a.page_size >= 16 && a.batch <= DecStream<128>::kMaxBatch &&
+         decode_group_size(a) <= DecStream<128>::kMaxGroup && a.k_stride[1] >= 0 &&
          a.k_stride[1] < lim && a.v_stride[1] >= 0 && a.v_stride[1] < lim;
+}
+
+// Resident waves per CU of the streaming kernel for head_dim D.
+static int stream_waves_per_cu(int D) {
+  switch (D) {
+    case 64: return DecStream<64>::kWavesPerCU;
+    case 256: return DecStream<256>::kWavesPerCU;
+  }
+  return DecStream<128>::kWavesPerCU;
 }
 
 // Keys per split.  The streaming kernel takes the largest of kSplitMax,
@@ -292,9 +302,9 @@ static int decode_split_size(const fa_decode_args& a) {
   if (!use_stream(a)) return dec_chunk(a.head_dim);
   const int G = a.num_heads / a.num_kv_heads;
   const int64_t heads = (int64_t)a.num_kv_heads * (G / decode_group_size(a));
-  const int64_t waves = (int64_t)device_cu_count() * DecStream::kWavesPerCU;
-  int s = DecStream::kSplitMax;
-  for (; s > DecStream::kSplitMin; s /= 2) {
+  const int64_t waves = (int64_t)device_cu_count() * stream_waves_per_cu(a.head_dim);
+  int s = tiles::kDecSplitKeysMax;
+  for (; s > tiles::kDecSplitKeysMin; s /= 2) {
     const int64_t items = (int64_t)a.batch * ((a.max_seq_len + s - 1) / s) * heads;
     if (items >= tiles::kDecItemsPerWave * waves) break;
   }
@@ -343,20 +353,17 @@ static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
   const int G = a.num_heads / a.num_kv_heads;
   const int64_t items = (int64_t)ws.nsplit * (G / GB) * a.num_kv_heads * a.batch;
   if (items > 0) {  // max_seq_len == 0: the combine alone writes zeros
-    if constexpr (D == 128) {
-      if (use_stream(a)) {
-        const int64_t wgs = std::max<int64_t>(
-            1, std::min<int64_t>((items + DecStream::kWavesPerWG - 1) / DecStream::kWavesPerWG,
-                                 (int64_t)device_cu_count() * DecStream::kWavesPerCU /
-                                     DecStream::kWavesPerWG));
-        DecodeWsS wss{ws.po, ws.plse, ws.split_dev, ws.nsplit, ws.split};
-        hipLaunchKernelGGL((decode_stream_kernel<T, GB>), dim3((unsigned)wgs),
-                           dim3(64 * DecStream::kWavesPerWG), 0,
-                           st, a, wss);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        return launch_combine<T, D>(a, ws, st);
-      }
+    if (D <= 256 && use_stream(a)) {
+      using SD = DecStream<D <= 256 ? D : 128>;
+      const int64_t wgs = std::max<int64_t>(
+          1, std::min<int64_t>((items + SD::kWavesPerWG - 1) / SD::kWavesPerWG,
+                               (int64_t)device_cu_count() * SD::kWavesPerCU / SD::kWavesPerWG));
+      DecodeWsS wss{ws.po, ws.plse, ws.split_dev, ws.nsplit, ws.split};
+      hipLaunchKernelGGL((decode_stream_kernel<T, SD::D, GB>), dim3((unsigned)wgs),
+                         dim3(64 * SD::kWavesPerWG), 0, st, a, wss);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      return launch_combine<T, D>(a, ws, st);
     }
     ws.split_dev = nullptr;  // the chunked kernel uses the launcher's split
     hipLaunchKernelGGL((decode_split_kernel<T, D, GB>), dim3((unsigned)items), dim3(256), 0, st,

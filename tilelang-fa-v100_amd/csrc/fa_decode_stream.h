@@ -1,20 +1,23 @@
-// Persistent streaming split-KV decode for head_dim 128 (gfx950).
+// Persistent streaming split-KV decode for head_dim 64 / 128 / 256 / 512
+// (gfx950).
 //
 // Work item = (sequence b, KV head, group of GB query heads, split c), one
 // split being kSplit consecutive keys.  Items are numbered sequence-major,
 // split-minor, so consecutive items continue the same key stream.  A
 // workgroup holds kWavesPerWG independent waves; each wave owns a contiguous
 // range of items and walks their keys in 16-key tiles:
-//  * every load reads whole 256-byte rows (16 lanes per row, 4 rows per
-//    instruction) with the non-temporal hint and goes straight to LDS
-//    (global_load_lds).  That pattern streams close to the HBM peak, whereas
+//  * every load reads whole rows (2D bytes: D / 8 lanes per row, 1024 / 2D
+//    rows per instruction) with the non-temporal hint and goes straight to
+//    LDS (global_load_lds).  That pattern streams close to the HBM peak, whereas
 //    64-byte pieces of 16 rows per instruction (the MFMA operand layout read
 //    from global memory directly) cost about 15% of it;
-//  * each wave has a two-tile LDS ring (K rows then V rows, 16-byte chunks
-//    XOR-swizzled per row so both the K row reads and the V transpose reads
-//    are conflict-free).  A tile is read into registers and its slot is
-//    refilled at once, so two tiles stay in flight while it is computed; one
-//    fixed vmcnt wait before the operand reads replaces any barrier;
+//  * each wave has an LDS ring of kDepth tiles (K rows then V rows, 16-byte
+//    chunks XOR-swizzled per row so the K row reads and the V transpose
+//    reads avoid bank conflicts).  A tile is read into registers and its
+//    slot is refilled at once, so kDepth tiles stay in flight while it is
+//    computed; one fixed vmcnt wait before the operand reads replaces any
+//    barrier.  Depth and waves per workgroup scale with D so that every
+//    head_dim keeps about 128 KB of K / V in flight per CU;
 //  * the page of a 16-key tile is wave-uniform (page size >= 16), so the
 //    block table is read with scalar loads, one tile ahead of its use;
 //  * S^T = K Q^T and O^T += V^T P^T both run on v_mfma_f32_16x16x32, with the
@@ -41,18 +44,32 @@
 
 namespace fa {
 
+template <int D_>
 struct DecStream {
-  static constexpr int D = 128;
+  static constexpr int D = D_;
   static constexpr int kSplitMax = tiles::kDecSplitKeysMax;  // keys per item, largest choice
   static constexpr int kSplitMin = tiles::kDecSplitKeysMin;  // smallest choice
   static constexpr int kTile = tiles::kDecTileKeys;        // keys per tile
-  static constexpr int kDepth = tiles::kDecTilesInFlight;  // tiles in the per-wave LDS ring
   static constexpr int kMaxBatch = 1024;
-  static constexpr int kWavesPerCU = 8;
-  static constexpr int kWavesPerWG = 8;
   static constexpr int kMaxGroup = 8;  // query heads per item (MFMA columns used)
   static constexpr int kRowBytes = D * 2;
   static constexpr int kTileBytes = 2 * kTile * kRowBytes;  // K rows, then V rows
+  static constexpr int kRowsPerDma = 1024 / kRowBytes;     // rows per DMA instruction
+  static constexpr int kLanesPerRow = 64 / kRowsPerDma;    // = D / 8, the row's chunks
+  static constexpr int kDmaPerTensor = kTile / kRowsPerDma;
+  static constexpr int kDmaPerTile = 2 * kDmaPerTensor;
+  // Tiles in flight per wave and waves per workgroup (one workgroup per CU,
+  // its LDS ring is 128 KB): D = 64: 4 x 4 KB x 8 waves; 128: 2 x 8 KB x 8;
+  // 256: 2 x 16 KB x 4; 512: 2 x 32 KB x 2.
+  static constexpr int kDepth = D == 128 ? tiles::kDecTilesInFlight : (D == 64 ? 4 : 2);
+  static constexpr int kWavesPerWG = D <= 128 ? 8 : 512 / D * 2;
+  static constexpr int kWavesPerCU = kWavesPerWG;
+  static constexpr int kWavesPerSimd = kWavesPerWG >= 8 ? 2 : 1;
+  // Query-slot rows: GB rounded up to whole DMA instructions.
+  static constexpr int kQueryRows = kMaxGroup > kRowsPerDma ? kMaxGroup : kRowsPerDma;
+  static constexpr int kSwzMask = D / 8 >= 16 ? 15 : D / 8 - 1;
+  static_assert(kRowsPerDma * kRowBytes == 1024 && kDmaPerTensor * kRowsPerDma == kTile, "DMA");
+  static_assert(kWavesPerWG * kDepth * kTileBytes == 128 * 1024, "LDS ring");
 };
 
 struct DecodeWsS {
@@ -96,7 +113,7 @@ __device__ __forceinline__ DecItem dec_item(int I, const int* pfx, const_i32_ptr
   it.hg = h % ngroups;
   it.n_begin = it.c * split;
   it.n_end = min(it.n_begin + split, len);
-  it.ntiles = (it.n_end - it.n_begin + DecStream::kTile - 1) / DecStream::kTile;
+  it.ntiles = (it.n_end - it.n_begin + tiles::kDecTileKeys - 1) / tiles::kDecTileKeys;
   return it;
 }
 
@@ -114,20 +131,21 @@ __device__ __forceinline__ void ld16_lds_nt(const void* g, char* lds) {
                                    /*nt*/ 2);
 }
 
-// Reads one tile's operands from LDS once its loads have landed: the four K
-// MFMA operands and, for each of the eight 16-wide d blocks, the V^T operand
-// (4 keys x 1 d per lane, ds_read_b64_tr_b16).  When a tile is read, the
-// only vector memory operations issued after its own 8 DMA instructions are
-// the next tile's 8, possibly a query-row DMA and partial-result stores; the
-// hardware counter completes in order, so vmcnt(8) means the tile (and a
+// Reads one tile's operands from LDS once its loads have landed: the D / 32
+// K MFMA operands and, for each of the D / 16 16-wide d blocks, the V^T
+// operand (4 keys x 1 d per lane, ds_read_b64_tr_b16).  When a tile is read,
+// the only vector memory operations issued after its own kDmaPerTile DMA
+// instructions are the later tiles' (kDepth - 1) x kDmaPerTile, possibly a
+// query-row DMA and partial-result stores; the hardware counter completes
+// in order, so vmcnt((kDepth - 1) x kDmaPerTile) means the tile (and a
 // query-row DMA issued before it) is resident.  The reads are opaque to the
 // compiler on purpose: its tracking of LDS DMA either waits for every
-// outstanding load or misses the dependence.
-__device__ __forceinline__ void lds_read_tile(uint32_t base, const int (&koff)[4],
-                                              const int (&voff)[8], u32x4 (&k)[4],
-                                              u32x2 (&v)[8]) {
+// outstanding load or misses the dependence.  They are issued in groups of
+// (4 K, 8 V) reads (2 and 4 at head_dim 64), each group one statement that
+// ends with its own lgkmcnt(0), so no result is used before it has landed.
+__device__ __forceinline__ void lds_read_k4v8(uint32_t base, const int* koff, const int* voff,
+                                              u32x4* k, u32x2* v) {
   asm volatile(
-      "s_waitcnt vmcnt(8)\n\t"
       "ds_read_b128 %0, %12\n\t"
       "ds_read_b128 %1, %13\n\t"
       "ds_read_b128 %2, %14\n\t"
@@ -148,29 +166,63 @@ __device__ __forceinline__ void lds_read_tile(uint32_t base, const int (&koff)[4
         "v"(base + voff[4]), "v"(base + voff[5]), "v"(base + voff[6]), "v"(base + voff[7])
       : "memory");
 }
+__device__ __forceinline__ void lds_read_k2v4(uint32_t base, const int* koff, const int* voff,
+                                              u32x4* k, u32x2* v) {
+  asm volatile(
+      "ds_read_b128 %0, %6\n\t"
+      "ds_read_b128 %1, %7\n\t"
+      "ds_read_b64_tr_b16 %2, %8\n\t"
+      "ds_read_b64_tr_b16 %3, %9\n\t"
+      "ds_read_b64_tr_b16 %4, %10\n\t"
+      "ds_read_b64_tr_b16 %5, %11\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(k[0]), "=&v"(k[1]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(base + koff[0]), "v"(base + koff[1]), "v"(base + voff[0]), "v"(base + voff[1]),
+        "v"(base + voff[2]), "v"(base + voff[3])
+      : "memory");
+}
+template <int D, int WAIT>
+__device__ __forceinline__ void lds_read_tile(uint32_t base, const int (&koff)[D / 32],
+                                              const int (&voff)[D / 16], u32x4 (&k)[D / 32],
+                                              u32x2 (&v)[D / 16]) {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
+  if constexpr (D == 64) {
+    lds_read_k2v4(base, koff, voff, k, v);
+  } else {
+#pragma unroll
+    for (int g = 0; g < D / 128; ++g)
+      lds_read_k4v8(base, koff + 4 * g, voff + 8 * g, k + 4 * g, v + 8 * g);
+  }
+}
 
 // Reads the B operand of S^T = K Q^T (query row l16, chunk 4c + grp) from the
 // wave's query slot.  The caller has made sure the slot's DMA has landed.
-__device__ __forceinline__ void lds_read_q(uint32_t base, const int (&qoff)[4], u32x4 (&q)[4]) {
-  asm volatile(
-      "ds_read_b128 %0, %4\n\t"
-      "ds_read_b128 %1, %5\n\t"
-      "ds_read_b128 %2, %6\n\t"
-      "ds_read_b128 %3, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
-      : "v"(base + qoff[0]), "v"(base + qoff[1]), "v"(base + qoff[2]), "v"(base + qoff[3])
-      : "memory");
+template <int D>
+__device__ __forceinline__ void lds_read_q(uint32_t base, const int (&qoff)[D / 32],
+                                           u32x4 (&q)[D / 32]) {
+#pragma unroll
+  for (int c = 0; c < D / 32; c += 2) {
+    if constexpr (D / 32 >= 2) {
+      asm volatile(
+          "ds_read_b128 %0, %2\n\t"
+          "ds_read_b128 %1, %3\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(q[c]), "=&v"(q[c + 1])
+          : "v"(base + qoff[c]), "v"(base + qoff[c + 1])
+          : "memory");
+    }
+  }
 }
 
-template <class T, int GB>
-__global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_kernel(
-    fa_decode_args a, DecodeWsS ws) {
-  using S = DecStream;
+template <class T, int D_, int GB>
+__global__ __launch_bounds__(DecStream<D_>::kWavesPerWG * 64, DecStream<D_>::kWavesPerSimd)
+void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
+  using S = DecStream<D_>;
   constexpr int D = S::D, TK = S::kTile, PD = S::kDepth, W = S::kWavesPerWG;
-  constexpr int RB = S::kRowBytes;
-  constexpr int QR = GB < 4 ? 4 : GB;  // query-slot rows (whole DMA instructions)
-  static_assert(PD == 2, "lds_read_tile assumes exactly one tile in flight behind the current one");
+  constexpr int RB = S::kRowBytes, RPD = S::kRowsPerDma, LPR = S::kLanesPerRow;
+  // Query-slot rows: GB rounded up to whole DMA instructions.
+  constexpr int QR = (GB + RPD - 1) / RPD * RPD;
+  static_assert(PD >= 2, "at least one tile in flight behind the current one");
   static_assert(GB <= S::kMaxGroup, "query slot holds kMaxGroup rows");
   __shared__ int pfx[S::kMaxBatch + 1];
   __shared__ __attribute__((aligned(16))) char ring[W][PD][S::kTileBytes];
@@ -239,15 +291,17 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   const unsigned last_page = (unsigned)(a.num_pages - 1);
   const int ks1 = (int)a.k_stride[1], vs1 = (int)a.v_stride[1];
 
-  // ---- per-lane constants.  DMA: instruction c fills rows 4c + grp, lane
-  // (l16, grp) chunk position l16 with chunk l16 ^ swz(row); offsets in
-  // elements from the tile's first row.
-  int kdma[TK / 4], vdma[TK / 4];
+  // ---- per-lane constants.  DMA: instruction c fills rows RPD c + dl, lane
+  // (dl = lane / LPR, pos = lane % LPR) chunk position pos with chunk
+  // pos ^ swz(row); offsets in elements from the tile's first row.
+  auto swz = [](int r) { return dec_swz(r) & S::kSwzMask; };
+  const int dl = lane / LPR, pos = lane % LPR;
+  int kdma[S::kDmaPerTensor], vdma[S::kDmaPerTensor];
 #pragma unroll
-  for (int c = 0; c < TK / 4; ++c) {
-    const int r = 4 * c + grp;
-    kdma[c] = r * ks1 + 8 * (l16 ^ dec_swz(r));
-    vdma[c] = r * vs1 + 8 * (l16 ^ dec_swz(r));
+  for (int c = 0; c < S::kDmaPerTensor; ++c) {
+    const int r = RPD * c + dl;
+    kdma[c] = r * ks1 + 8 * (pos ^ swz(r));
+    vdma[c] = r * vs1 + 8 * (pos ^ swz(r));
   }
   // LDS operand offsets within a ring slot.  K (A operand c of S^T): row l16,
   // chunk 4c + grp.  V^T (A operand of O^T, d block db): lane (k = l16, grp)
@@ -255,16 +309,16 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   // the transpose read hands lane (l16, grp) V[4 grp + j][16 db + l16], j < 4.
   int koff[D / 32], voff[D / 16];
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) koff[c] = l16 * RB + 16 * ((4 * c + grp) ^ dec_swz(l16));
+  for (int c = 0; c < D / 32; ++c) koff[c] = l16 * RB + 16 * ((4 * c + grp) ^ swz(l16));
   {
     const int r = 4 * grp + (l16 >> 2);
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
       const int chunk = 2 * db + ((l16 & 3) >> 1);
-      voff[db] = TK * RB + r * RB + 16 * (chunk ^ dec_swz(r)) + 8 * (l16 & 1);
+      voff[db] = TK * RB + r * RB + 16 * (chunk ^ swz(r)) + 8 * (l16 & 1);
     }
   }
-  // Query slot: row h (head h0 + h) holds its 256 bytes unswizzled; the B
+  // Query slot: row h (head h0 + h) holds its RB bytes unswizzled; the B
   // operand c of S^T for column l16 is chunk 4c + grp of row l16 (columns
   // >= GB read row 0 and are zeroed after the read).
   int qoff[D / 32];
@@ -274,8 +328,8 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   const uint32_t q_base = lds_addr(qslot[wv][0]);
 
   // ---- producer.  prepare() computes the addresses of tile (pI, pt) and
-  // advances to the next tile; issue(slot) then puts its 8 DMA instructions
-  // (4 rows of 256 bytes each) into ring slot `slot`.  The split lets the
+  // advances to the next tile; issue(slot) then puts its kDmaPerTile DMA
+  // instructions (RPD rows each) into ring slot `slot`.  The split lets the
   // address work run before the wait for the tile being replaced, so only
   // the DMA issue separates that tile's arrival from the refill.  Every
   // issue() emits the 8 instructions (after the last tile it reloads that
@@ -329,24 +383,24 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
   auto issue = [&](int slot) {
     if (q_src) {
 #pragma unroll
-      for (int r0 = 0; r0 < QR; r0 += 4)
-        ld16_lds_nt(q_src + (int64_t)(q_h0 + min(r0 + grp, GB - 1)) * a.q_stride[1] + 8 * l16,
+      for (int r0 = 0; r0 < QR; r0 += RPD)
+        ld16_lds_nt(q_src + (int64_t)(q_h0 + min(r0 + dl, GB - 1)) * a.q_stride[1] + 8 * pos,
                     qslot[wv][r0]);
     }
     char* kb = ring[wv][slot];
     char* vb = kb + TK * RB;
     if (dr_n == TK - 1) {
 #pragma unroll
-      for (int c = 0; c < TK / 4; ++c) {
+      for (int c = 0; c < S::kDmaPerTensor; ++c) {
         ld16_lds_nt(kc_n + kdma[c], kb + 1024 * c);
         ld16_lds_nt(vc_n + vdma[c], vb + 1024 * c);
       }
     } else {  // last tile of the item: rows past its end repeat the last key
 #pragma unroll
-      for (int c = 0; c < TK / 4; ++c) {
-        const int r = 4 * c + grp;
+      for (int c = 0; c < S::kDmaPerTensor; ++c) {
+        const int r = RPD * c + dl;
         const int dr = min(r, dr_n);
-        const int j = 8 * (l16 ^ dec_swz(r));
+        const int j = 8 * (pos ^ swz(r));
         ld16_lds_nt(kc_n + dr * ks1 + j, kb + 1024 * c);
         ld16_lds_nt(vc_n + dr * vs1 + j, vb + 1024 * c);
       }
@@ -368,7 +422,7 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
     if (q_item == cI) {
       // DMA issued with this item's first tile, before it: resident once
       // that tile has passed its wait.
-      lds_read_q(q_base, qoff, qb);
+      lds_read_q<D>(q_base, qoff, qb);
       q_item = -1;
     } else {
       // The slot holds a later item's rows: read this item's rows directly.
@@ -467,7 +521,8 @@ __global__ __launch_bounds__(DecStream::kWavesPerWG * 64, 2) void decode_stream_
       // Pins the prepared addresses ahead of the wait (volatile asm keeps its
       // order; the compiler would otherwise sink the address work past it).
       asm volatile("" ::"s"(kc_n), "s"(vc_n), "s"(dr_n), "s"(q_src));
-      lds_read_tile(ring_base + s * S::kTileBytes, koff, voff, kr, vt);
+      lds_read_tile<D, (PD - 1) * S::kDmaPerTile>(ring_base + s * S::kTileBytes, koff, voff, kr,
+                                                  vt);
       issue(s);
       if (cI < I1) consume(kr, vt);
     }
