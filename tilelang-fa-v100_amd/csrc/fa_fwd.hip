@@ -211,48 +211,46 @@ struct PagedSplitRows : PagedRows {
 
 // Finds the sequence owning `tile` in the varlen tile space where sequence b
 // has ceil(qlen_b * G / BM) tiles.  Returns b (or -1) and the tile index
-// within the sequence.  Threads 0..255 scan query_start_loc in LDS, 256
-// sequences per pass; the rest of the workgroup only joins the barriers.
+// within the sequence.  Wave 0 scans query_start_loc 64 sequences at a time
+// with a shuffle prefix sum and finds the owner with a ballot; one barrier
+// hands the result to the other waves (a block-wide scan in LDS took 16
+// barriers).
 __device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
                              int tile, int* local) {
-  constexpr int NS = 256;
-  __shared__ int scan[NS];
-  __shared__ int found_b, found_local, chunk_total;
-  const int tid = threadIdx.x;
-  const bool act = tid < NS;
-  if (tid == 0) {
-    found_b = -1;
-    found_local = 0;
+  __shared__ int found_b, found_local;
+  if (wave_id() == 0) {
+    const int lane = threadIdx.x & 63;
+    int base = 0, fb = -1, fl = 0;
+    for (int c0 = 0; c0 < batch; c0 += 64) {
+      const int b = c0 + lane;
+      int n = 0;
+      if (b < batch) {
+        const int ql = qsl[b + 1] - qsl[b];
+        n = ql > 0 ? (int)(((int64_t)ql * G + BM - 1) / BM) : 0;
+      }
+      int incl = n;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
+      }
+      const int excl = incl - n;
+      const bool hit = b < batch && n > 0 && tile >= base + excl && tile < base + incl;
+      const uint64_t m = __ballot(hit);
+      if (m) {
+        const int src = __ffsll((unsigned long long)m) - 1;
+        fb = c0 + src;
+        fl = tile - base - __shfl(excl, src);
+        break;
+      }
+      base += __shfl(incl, 63);
+    }
+    if (lane == 0) {
+      found_b = fb;
+      found_local = fl;
+    }
   }
   __syncthreads();
-  int base = 0;
-  for (int c0 = 0; c0 < batch; c0 += NS) {
-    const int b = c0 + tid;
-    int n = 0;
-    if (act && b < batch) {
-      const int ql = qsl[b + 1] - qsl[b];
-      n = ql > 0 ? (int)(((int64_t)ql * G + BM - 1) / BM) : 0;
-    }
-    if (act) scan[tid] = n;
-    __syncthreads();
-    for (int off = 1; off < NS; off <<= 1) {
-      const int add = (act && tid >= off) ? scan[tid - off] : 0;
-      __syncthreads();
-      if (act) scan[tid] += add;
-      __syncthreads();
-    }
-    const int incl = act ? scan[tid] : 0;
-    const int excl = incl - n;
-    if (act && b < batch && n > 0 && tile >= base + excl && tile < base + incl) {
-      found_b = b;
-      found_local = tile - base - excl;
-    }
-    if (tid == NS - 1) chunk_total = incl;
-    __syncthreads();
-    if (found_b >= 0) break;
-    base += chunk_total;
-    __syncthreads();
-  }
   *local = found_local;
   return found_b;
 }
