@@ -10,7 +10,7 @@ value = algorithmic FLOPs per step / step time (FLOPs over unmasked pairs
 only: fwd 4*D*H*pairs, bwd 2.5x fwd).
 
 `roofline` covers the dominant launch of that step, the fa_bwd call (its
-pre / main / dQ-convert kernels), timed with HIP events on the stream it is
+statistics, dK / dV and dQ kernels), timed with HIP events on the stream it is
 launched on; its `traffic` (HBM bytes per launch) comes from the counter
 runs summarised in profiles/fa_bwd_c2_traffic.md.  `extra` reports the other
 BASELINE configs and the north-star points (T1: S=8192 fwd+bwd, T2: decode
@@ -291,26 +291,16 @@ def headline(fa, steps, warmup, dev):
         _lib.check(lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), nbytes, stream), "fa_bwd")
 
     bwd_ms, bwd_api = time_reps(bwd, max(steps, 20), 3)
-    # The same launch with deterministic=1 (query-stationary dQ, no atomics).
-    a_det = _dense.bwd_args(qd, kd, vd, out, do, lse, dq, dk, dv, D ** -0.5, True, True)
-    nb_det = lib.fa_bwd_workspace_bytes(ctypes.byref(a_det))
-    ws_det = torch.empty(nb_det, dtype=torch.uint8, device=dev)
-
-    def bwd_det():
-        _lib.check(lib.fa_bwd(ctypes.byref(a_det), ws_det.data_ptr(), nb_det, stream), "fa_bwd")
-
-    det_ms, det_api = time_reps(bwd_det, max(steps, 20), 3)
     fwd_ms, fwd_api = time_reps(lambda: _dense.forward(qd, kd, vd, D ** -0.5, True),
                                 max(steps, 20), 3)
     bwd_tf = 2.5 * f_fwd / (bwd_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(bwd_tf, 1), "peak": PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(bwd_tf / PEAK_TFLOPS, 4),
                 "traffic": profiled_traffic("fa_bwd_c2"),
-                "kernel": "fa_bwd (bwd_pre + bwd_main + bwd_dq_convert)",
+                "kernel": "fa_bwd (bwd_pre + bwd_main_mfma dK/dV + bwd_dq dQ)",
                 "launch_ms": round(bwd_ms, 4), "algorithmic_gflop": round(2.5 * f_fwd / 1e9, 2)}
     parts = dict([flop_entry("C2_fwd", f_fwd, fwd_ms, fwd_api),
-                  flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms, bwd_api),
-                  flop_entry("C2_bwd_deterministic", 2.5 * f_fwd, det_ms, det_api)])
+                  flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms, bwd_api)])
     return ms, f_step, roofline, parts
 
 
@@ -335,14 +325,6 @@ def extras(fa, dev, reps):
 
     ms, api = time_reps(t1, max(reps // 2, 5), 2)
     res.update([flop_entry("T1_fwd_bwd", 3.5 * f_fwd, ms, api)])
-
-    def t1_det():
-        q.grad = k.grad = v.grad = None
-        o = fa.tilelang_flash_attn_func(q, k, v, causal=True, deterministic=True)
-        o.backward(do)
-
-    ms, api = time_reps(t1_det, max(reps // 2, 5), 2)
-    res.update([flop_entry("T1_fwd_bwd_deterministic", 3.5 * f_fwd, ms, api)])
     ms, api = time_reps(lambda: fa.tilelang_flash_attn_func(q.detach(), k.detach(), v.detach(),
                                                           causal=True), reps, 3)
     res.update([flop_entry("T1_fwd", f_fwd, ms, api)])

@@ -320,16 +320,30 @@ def test_deterministic_backward_matches_oracle_and_repeats(case):
             assert rel_l2(got, want) < 1e-2, name
 
 
-def test_deterministic_and_atomic_paths_agree():
-    """Both backward paths compute the same gradients (to fp32 summation
-    order): dk / dv come from the same kernel code, dq from either reduction."""
-    g = torch.Generator().manual_seed(22)
-    q, k, v, do = (randn(g, 2, 1000, 8, 128) for _ in range(4))
+def _grads_both_flags(d, seed):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v, do = (randn(g, 2, 1000, 8, d) for _ in range(4))
     res = []
     for det in (False, True):
         qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
         out = fa.tilelang_flash_attn_func(qd, kd, vd, causal=True, deterministic=det)
         out.backward(do.to(DEV))
         res.append((qd.grad.float(), kd.grad, vd.grad))
+    return res
+
+
+def test_deterministic_and_atomic_paths_agree():
+    """head_dim 256 has both backward paths: the same gradients up to fp32
+    summation order; dk / dv come from the same kernel code, dq from either
+    reduction."""
+    res = _grads_both_flags(256, 22)
     assert torch.equal(res[0][1], res[1][1]) and torch.equal(res[0][2], res[1][2])
     assert (res[0][0] - res[1][0]).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_atomic_free_path_is_the_default_below_256(d):
+    """head_dim 64 / 128 always take the atomic-free path: deterministic=False
+    gives the deterministic=True gradients bit for bit."""
+    res = _grads_both_flags(d, 23)
+    assert all(torch.equal(x, y) for x, y in zip(res[0], res[1]))

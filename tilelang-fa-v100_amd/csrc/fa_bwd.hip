@@ -6,22 +6,28 @@
 // GEMMs per tile pair); here one KV-stationary kernel does the 5 GEMMs
 //   S = Q K^T,  dP = dO V^T,  dV += P^T dO,  dK += dS^T Q,  dQ += dS K
 // with P = exp(scale*S - lse), dS = P * (dP - rowdot(O, dO))
-// (_kernels_backward.py:72-74,159-170).  dQ is reduced across KV tiles with
-// fp32 atomics into a caller-provided workspace and converted afterwards.
-//
-// dQ is accumulated in fp32 in a [B, H, Sq, D] workspace.
+// (_kernels_backward.py:72-74,159-170).  Two ways to obtain dQ:
+//  * atomic-free (head_dim 64 and 128, and any head_dim when `deterministic`
+//    is set): the key-stationary kernel computes S, dP, dV, dK and a
+//    query-stationary kernel (fa_bwd_dq.h) recomputes S and dP per query
+//    tile and builds each dQ row in one wave, like the reference's dQ kernel;
+//  * atomic (head_dim 256 unless `deterministic`): the key-stationary kernel
+//    also computes dQ += dS K and reduces it across key tiles with fp32
+//    atomics into a [B, H, Sq, D] workspace, converted afterwards.
 //
 // Kernels:
 //   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row; zeroes
-//                       the dQ accumulator rows it covers.  Both statistics
-//                       live in one array [B*H][2][Sq] (LSE*log2(e) first,
-//                       rowdot second), so a lane addresses either with a
-//                       32-bit offset from a per-head base.
-//   bwd_main_kernel     workgroup = 128 keys (32 per wave) of one KV head;
-//                       loops over the 64-row query tiles of every query
-//                       head that shares the KV head (GQA).  K and V of the wave stay in registers,
-//                       K^T of the workgroup stays in LDS.
+//                       the dQ accumulator rows it covers (atomic path).  Both
+//                       statistics live in one array [B*H][2][Sq]
+//                       (LSE*log2(e) first, rowdot second), so a lane
+//                       addresses either with a 32-bit offset from a
+//                       per-head base.
+//   bwd_main_kernel     head_dim 64: workgroup = 128 keys (32 per wave) of one
+//                       KV head; loops over the 64-row query tiles of every
+//                       query head that shares the KV head (GQA).  K and V of
+//                       the wave stay in registers.
 //   bwd_main_mfma_kernel  head_dim 128 / 256 variant (fa_bwd_mfma.h).
+//   bwd_dq_kernel       query-stationary dQ (fa_bwd_dq.h).
 //   bwd_dq_convert      dQ = scale * acc, cast to the input dtype.
 #include "fa_bwd_dq.h"
 #include "fa_bwd_mfma.h"
@@ -41,15 +47,11 @@ struct BwdShape {
   static constexpr int RG = BQ * CPR / 256;  // consecutive rows per thread
   static constexpr int QS = D + 8;        // natural Q / dO row stride
   static constexpr int TS = BQ + 4;       // transposed Q / dO row stride
-  static constexpr int SS = BKV + 8;      // dS row stride
-  static constexpr int KTS = BKV + 8;     // K^T row stride
   static constexpr int OFF_QS = 0;
   static constexpr int OFF_DOS = OFF_QS + BQ * QS;
   static constexpr int OFF_QT = OFF_DOS + BQ * QS;
   static constexpr int OFF_DOT = OFF_QT + D * TS;
-  static constexpr int OFF_DS = OFF_DOT + D * TS;
-  static constexpr int OFF_KT = OFF_DS + BQ * SS;
-  static constexpr int LDS_ELEMS = OFF_KT + D * KTS;
+  static constexpr int LDS_ELEMS = OFF_DOT + D * TS;
   static_assert(RG == 2 || RG == 4, "row grouping");
 };
 
@@ -116,12 +118,10 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 }
 
 // ------------------------------------------------------------ main kernel
-// MODE (MaskMode): full attention, causal, or a window band from the
-// arguments.  DQ: also compute dQ (fp32 atomics into dqacc); without it the
-// kernel writes dK / dV only (deterministic path, dQ from bwd_dq_kernel).
-template <class T, int D, int MODE, bool DQ>
-__global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqacc,
-                                                       const float* stats) {
+// head_dim 64: dK / dV only (dQ comes from bwd_dq_kernel).  MODE (MaskMode):
+// full attention, causal, or a window band from the arguments.
+template <class T, int D, int MODE>
+__global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const float* stats) {
   using S = BwdShape<D>;
   constexpr bool CAUSAL = MODE != kMaskNone;  // some (query, key) pairs are outside the band
   __shared__ __attribute__((aligned(16))) uint16_t smem[S::LDS_ELEMS];
@@ -131,8 +131,6 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
   uint16_t* dOs = smem + S::OFF_DOS;
   uint16_t* Qt = smem + S::OFF_QT;
   uint16_t* dOt = smem + S::OFF_DOT;
-  uint16_t* dSs = smem + S::OFF_DS;
-  uint16_t* Kt = smem + S::OFF_KT;
 
   const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads, Hk = a.num_heads_k;
   const int G = H / Hk;  // query heads sharing this KV head
@@ -153,7 +151,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
 
-  // ---- stationary operands: K, V rows of this lane (B operands), K^T in LDS.
+  // ---- stationary operands: K, V rows of this lane (B operands).
   u32x4 kB[S::DC], vB[S::DC];
   {
     const bool ok = my_kv < Sk;
@@ -163,27 +161,6 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     for (int c = 0; c < S::DC; ++c) {
       kB[c] = ok ? ld16(kp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
       vB[c] = ok ? ld16(vp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
-    }
-    const int col8 = tid % S::CPR, grp = tid / S::CPR;
-    constexpr int GPP = 256 / S::CPR;  // 4-row groups per pass
-#pragma unroll
-    for (int p = 0; p < (DQ ? S::BKV / (4 * GPP) : 0); ++p) {
-      const int rbase = 4 * (grp + GPP * p);
-      u32x4 rows[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = kv0 + rbase + r;
-        rows[r] = n < Sk ? ld16(kg + (int64_t)n * a.k_stride[1] + 8 * col8)
-                         : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int w = j >> 1;
-        u32x2 pr;
-        pr[0] = (j & 1) ? pack_hi(rows[0][w], rows[1][w]) : pack_lo(rows[0][w], rows[1][w]);
-        pr[1] = (j & 1) ? pack_hi(rows[2][w], rows[3][w]) : pack_lo(rows[2][w], rows[3][w]);
-        st8(Kt + (8 * col8 + j) * S::KTS + rbase, pr);
-      }
     }
   }
 
@@ -263,9 +240,8 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
     store_q();
   }
   for (int t = 0; t < ntot; ++t) {
-    const int h = hk * G + t / nit;
     const int i0 = (it0 + t % nit) * S::BQ;
-    __syncthreads();  // Q/dO tile (and K^T on the first pass) visible
+    __syncthreads();  // Q/dO tile visible
     const bool more = t + 1 < ntot;
     if (more) load_q(t + 1);
 
@@ -309,7 +285,7 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
             dp[qt][i] = p * (dp[qt][i] - d4[r]);  // dS (unscaled)
           }
         }
-      // Pack P and dS as B operands; write dS to LDS for the dQ product.
+      // Pack P and dS as B operands.
       u32x4 pB[2 * S::NQT], sB[2 * S::NQT];
 #pragma unroll
       for (int kq = 0; kq < 2 * S::NQT; ++kq)
@@ -318,17 +294,6 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
           const int e = 8 * (kq & 1) + 2 * w;
           pB[kq][w] = T::pack(s[kq >> 1][e], s[kq >> 1][e + 1]);
           sB[kq][w] = T::pack(dp[kq >> 1][e], dp[kq >> 1][e + 1]);
-        }
-#pragma unroll
-      for (int kq = 0; kq < (DQ ? 2 * S::NQT : 0); ++kq)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          // halves of sB[kq][w] are entries e, e+1 = rows qrow, qrow+1
-          const int e = 8 * (kq & 1) + 2 * w;
-          const int qrow = (kq >> 1) * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
-          const uint32_t v = sB[kq][w];
-          dSs[qrow * S::SS + 32 * wave + lr] = (uint16_t)(v & 0xffffu);
-          dSs[(qrow + 1) * S::SS + 32 * wave + lr] = (uint16_t)(v >> 16);
         }
       // dV^T += dO^T P,  dK^T += Q^T dS
 #pragma unroll
@@ -345,40 +310,9 @@ __global__ __launch_bounds__(256) void bwd_main_kernel(fa_bwd_args a, float* dqa
           dv[dt] = T::mma32(ad, pB[kq], dv[dt]);
           dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
         }
-    } else if constexpr (DQ) {
-      // Inactive waves contribute zero dS to the shared dQ product.
-#pragma unroll
-      for (int q = 0; q < S::BQ; ++q) dSs[q * S::SS + 32 * wave + lr] = 0;
     }
-    __syncthreads();  // dS complete; Q/dO tiles no longer read
+    __syncthreads();  // Q/dO tiles no longer read
     if (more) store_q();
-
-    // dQ[i0 + q][d] += sum_k dS[q][k] K[k][d] over this workgroup's 128 keys.
-    {
-      const bool any = !CAUSAL || band.any(i0, i0 + S::BQ - 1, kv0, kv0 + S::BKV - 1);
-      if (DQ && any) {
-        float* dqb = dqacc + ((int64_t)b * H + h) * Sq * D;  // [B, H, Sq, D]
-        const int64_t qstride = D;
-#pragma unroll
-        for (int pr = wave; pr < S::NQT * S::DT; pr += 4) {
-          const int qt = pr % S::NQT, dt = pr / S::NQT;
-          f32x16 acc;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-#pragma unroll
-          for (int kc = 0; kc < S::BKV / 16; ++kc) {
-            const u32x4 as = ld16(dSs + (qt * 32 + lr) * S::SS + 16 * kc + 8 * lh);
-            const u32x4 bk = ld16(Kt + (dt * 32 + lr) * S::KTS + 16 * kc + 8 * lh);
-            acc = T::mma32(as, bk, acc);
-          }
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int qi = i0 + qt * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
-            if (qi < Sq) unsafeAtomicAdd(dqb + qi * qstride + dt * 32 + lr, acc[i]);
-          }
-        }
-      }
-    }
   }
 
   // ---- epilogue: this lane's key row.
@@ -446,18 +380,26 @@ __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(fa_bwd_args a,
 
 // ----------------------------------------------------------------- launchers
 
+// dQ by fp32 atomics (head_dim 256 unless `deterministic`) or by the
+// query-stationary kernel.
+static bool bwd_atomic_dq(const fa_bwd_args& a) {
+  return !a.deterministic && a.head_dim >= tiles::kBwdAtomicMinHeadDim;
+}
+
 // Workspace: the fp32 dQ accumulator [B, H, Sq, D] (atomic path only), then
 // the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot).
 size_t bwd_workspace_bytes(const fa_bwd_args& a) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
-  const size_t acc = a.deterministic ? 0 : rows * a.head_dim * sizeof(float);
+  const size_t acc = bwd_atomic_dq(a) ? rows * a.head_dim * sizeof(float) : 0;
   return acc + 2 * rows * sizeof(float) + 256;
 }
 
-// Key-stationary main kernel for one mask mode; DQ selects the atomic dQ.
+// Key-stationary main kernel for one mask mode; DQ selects the atomic dQ
+// (head_dim 256 only).
 template <class T, int D, bool DQ>
 static void launch_bwd_main(const fa_bwd_args& a, int mode, float* dqacc, const float* stats,
                             hipStream_t st) {
+  static_assert(!DQ || D >= tiles::kBwdAtomicMinHeadDim, "atomic dQ path");
   if constexpr (D >= 128) {
     constexpr int KB = D == 128 ? kBwdKB : 1;
     using S2 = BwdShapeMfma<D, KB>;
@@ -479,14 +421,11 @@ static void launch_bwd_main(const fa_bwd_args& a, int mode, float* dqacc, const 
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch);
     if (kvtiles == 0) return;
     if (mode == kMaskCausal)
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskCausal, DQ>), grid, dim3(256), 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskCausal>), grid, dim3(256), 0, st, a, stats);
     else if (mode == kMaskBand)
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskBand, DQ>), grid, dim3(256), 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskBand>), grid, dim3(256), 0, st, a, stats);
     else
-      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskNone, DQ>), grid, dim3(256), 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_kernel<T, D, kMaskNone>), grid, dim3(256), 0, st, a, stats);
   }
 }
 
@@ -504,33 +443,37 @@ static void launch_bwd_dq(const fa_bwd_args& a, int mode, const float* stats, hi
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
 }
 
-// Default path: pre (statistics, zeroed accumulator), main with fp32 dQ
-// atomics, dQ convert.  Deterministic path: pre (statistics), main without
-// dQ, then the query-stationary dQ kernel, which writes dQ directly; every
-// output element is then produced by one fixed sequence of operations.
+// Atomic-free path: pre (statistics), main without dQ, then the
+// query-stationary dQ kernel, which writes dQ directly; every output element
+// is produced by one fixed sequence of operations.  Atomic path (head_dim 256
+// unless `deterministic`): pre (statistics, zeroed accumulator), main with
+// fp32 dQ atomics, dQ convert.
 template <class T, int D>
 static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
-  const bool det = a.deterministic != 0;
-  float* dqacc = det ? nullptr : static_cast<float*>(ws);
-  float* stats = static_cast<float*>(ws) + (det ? 0 : rows * D);  // [B*H][2][Sq]
+  constexpr bool kCanAtomic = D >= tiles::kBwdAtomicMinHeadDim;
+  const bool atomic = kCanAtomic && bwd_atomic_dq(a);
+  float* dqacc = atomic ? static_cast<float*>(ws) : nullptr;
+  float* stats = static_cast<float*>(ws) + (atomic ? rows * D : 0);  // [B*H][2][Sq]
   const dim3 rgrid((unsigned)((a.seqlen_q + pre_rows_per_block<D>() - 1) / pre_rows_per_block<D>()),
                    (unsigned)(a.batch * a.num_heads));
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int mode = mask_mode(a);
-  if (det) {
-    launch_bwd_main<T, D, false>(a, mode, nullptr, stats, st);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    launch_bwd_dq<T, D>(a, mode, stats, st);
-    return hipGetLastError();
+  if constexpr (kCanAtomic) {
+    if (atomic) {
+      launch_bwd_main<T, D, true>(a, mode, dqacc, stats, st);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((bwd_dq_convert_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc);
+      return hipGetLastError();
+    }
   }
-  launch_bwd_main<T, D, true>(a, mode, dqacc, stats, st);
+  launch_bwd_main<T, D, false>(a, mode, nullptr, stats, st);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_dq_convert_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc);
+  launch_bwd_dq<T, D>(a, mode, stats, st);
   return hipGetLastError();
 }
 

@@ -1,18 +1,20 @@
 // Attention backward main kernel for head_dim 128 and 256 on gfx950.
 //
 // Same mathematics as bwd_main_kernel (fa_bwd.hip): per (key tile, query
-// tile) the 5 products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS and
-// dQ += dS K, with P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot).
+// tile) the products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS and,
+// on the atomic path (DQ = true, head_dim 256 only), dQ += dS K, with
+// P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot).
 // Layout, for the gfx950 memory instructions:
-//  * D = 128: 256 keys per workgroup, NW = 8 / KB waves, each owning KB
-//    blocks of 32 keys.  The fp32 atomics that reduce dQ across key tiles
-//    then cover 256 keys each, and every Q / dO tile fetched into LDS serves
-//    256 keys.  With KB = 2 (4 waves, one per SIMD) a wave has 512
-//    registers, holds dK / dV of 64 keys, and every Q / dO operand it reads
-//    from LDS feeds the products of both its key blocks.
+//  * D = 128 (dK / dV only; dQ from bwd_dq_kernel): 256 keys per
+//    workgroup, NW = 8 / KB waves, each owning KB blocks of 32 keys, so every
+//    Q / dO tile fetched into LDS serves 256 keys.  With KB = 2 (4 waves, one
+//    per SIMD) a wave has 512 registers, holds dK / dV of 64 keys, and every
+//    Q / dO operand it reads from LDS feeds the products of both its key
+//    blocks.
 //  * D = 256: 128 keys per workgroup, 4 waves x 32 keys, one wave per SIMD
 //    (dK / dV of 32 keys x 256 d take 256 registers); rows are 512 bytes,
-//    and each wave computes two 32-wide d tiles of dQ.
+//    and on the atomic path each wave computes two 32-wide d tiles of dQ,
+//    which the fp32 atomics then reduce across key tiles.
 //  * The workgroup's K tile (BKV x 2D bytes) is copied once HBM -> LDS with
 //    global_load_lds_dwordx4 and serves as the B operand of S (row reads)
 //    and of dQ (transpose reads).  V rows of each wave stay in registers.

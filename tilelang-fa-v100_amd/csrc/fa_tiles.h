@@ -59,6 +59,19 @@ constexpr int kFwdCoreKeys512 = 32;
 constexpr int kBwd128KeyBlocksPerWave = 1;
 constexpr int kBwdQueryRows = 32;
 
+// ---- backward: how dQ is reduced over key tiles (fa_bwd.hip).  head_dim
+// below kBwdAtomicMinHeadDim always takes the atomic-free path (query-
+// stationary dQ kernel); at and above it, fp32 atomics unless deterministic.
+// Evidence (fa_bwd per call, ms, atomic / atomic-free, fp16, one process):
+// D=64 B4 S2048 H16 causal 0.405 / 0.343, full 0.523 / 0.443; D=128 C2 causal
+// 0.314 / 0.300, full 0.521 / 0.507, T1 1.811 / 1.814, GQA 32/8 B2 S4096
+// causal 1.283 / 1.224, full 1.733 / 1.772, B1 S16384 H8 1.767 / 1.777, B8
+// S1024 0.203 / 0.208; D=256 B2 S8192 H8 causal 3.471 / 3.562, B2 S4096 full
+// 1.667 / 1.751.  (The atomic kernel's dQ updates are performed beyond the
+// XCD's L2 on this part and cost ~64 address cycles per instruction, a floor
+// of ~1.17 ms for T1's backward.)
+constexpr int kBwdAtomicMinHeadDim = 256;
+
 // ---- backward main kernel, head_dim 64 (fa_bwd.hip)
 // 128 keys per workgroup, 64 query rows per iteration, 4 waves.
 constexpr int kBwd64Keys = 128;
