@@ -97,9 +97,7 @@ int fa_fwd(const fa_fwd_args* args, void* stream);
 
 /* Backward: LSE-recompute FlashAttention-2 gradient.  dq/dk/dv use the same
  * layout rules as q/k/v.  Workspace holds the per-row statistics (LSE and
- * dot(O, dO)) and, on the atomic path (head_dim 256 without `deterministic`),
- * an fp32 dQ accumulator; its size comes from fa_bwd_workspace_bytes (it
- * depends on head_dim and that flag). */
+ * dot(O, dO)); its size comes from fa_bwd_workspace_bytes. */
 typedef struct fa_bwd_args {
   const void* q;
   const void* k;
@@ -127,14 +125,12 @@ typedef struct fa_bwd_args {
   float softmax_scale;
   int32_t causal;
   int32_t dtype;
-  int32_t deterministic; /* 1, and always at head_dim 64 / 128: a
-                          * query-stationary dQ kernel writes each dq row once,
-                          * so dq, dk and dv repeat bit for bit (as the
-                          * reference's atomic-free kernels,
-                          * _kernels_backward.py:10-85,88-176, always do);
-                          * 0 at head_dim 256: dQ summed over key tiles with
-                          * fp32 atomics, whose order varies run to run (the
-                          * last bits of dq may differ) */
+  int32_t deterministic; /* accepted and ignored, as in the reference
+                          * (interface.py:16-17): the backward has no atomics
+                          * (a query-stationary kernel writes each dq row
+                          * once), so dq, dk and dv always repeat bit for bit,
+                          * like the reference's kernels
+                          * (_kernels_backward.py:10-85,88-176) */
   int32_t has_window;    /* as in fa_fwd_args */
   int32_t window_left;
   int32_t window_right;

@@ -27,6 +27,14 @@ SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_decode.hip", "fa_cache.hip", "fa_scra
            "fa_capi.cpp"]
 ARCH = "gfx950"
 
+# Per-source flags.  fa_bwd.hip: MFMA results in VGPRs.  Its head_dim 256
+# dK / dV kernel holds dK / dV in the 256 accumulator registers; with the
+# default heuristic the S / dP accumulators were placed there too and 32 of
+# them spilled to scratch every tile (T1-shape head_dim 256 backward 3.54 ms,
+# 2.41 ms in this form).  The head_dim 64 / 128 kernels compile to the same
+# code either way.
+SOURCE_FLAGS = {"fa_bwd.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+
 COMMON_FLAGS = [
     "-O3",
     "-std=c++17",
@@ -76,7 +84,8 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
     for src in SOURCES:
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmds.append([cc, *flags, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([cc, *flags, *SOURCE_FLAGS.get(src, []), "-x", "hip", "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 4)) as ex:
         for fut in [ex.submit(_run, c, verbose) for c in cmds]:
             fut.result()

@@ -6,29 +6,25 @@
 // GEMMs per tile pair); here one KV-stationary kernel does the 5 GEMMs
 //   S = Q K^T,  dP = dO V^T,  dV += P^T dO,  dK += dS^T Q,  dQ += dS K
 // with P = exp(scale*S - lse), dS = P * (dP - rowdot(O, dO))
-// (_kernels_backward.py:72-74,159-170).  Two ways to obtain dQ:
-//  * atomic-free (head_dim 64 and 128, and any head_dim when `deterministic`
-//    is set): the key-stationary kernel computes S, dP, dV, dK and a
-//    query-stationary kernel (fa_bwd_dq.h) recomputes S and dP per query
-//    tile and builds each dQ row in one wave, like the reference's dQ kernel;
-//  * atomic (head_dim 256 unless `deterministic`): the key-stationary kernel
-//    also computes dQ += dS K and reduces it across key tiles with fp32
-//    atomics into a [B, H, Sq, D] workspace, converted afterwards.
+// (_kernels_backward.py:72-74,159-170).  dQ comes from a query-stationary
+// kernel (fa_bwd_dq.h) that recomputes S and dP per query tile and builds
+// each dQ row in one wave, like the reference's dQ kernel: no atomics, so
+// dq, dk and dv repeat bit for bit (fp32 atomics into a dQ accumulator were
+// measured slower at every head_dim: they are performed beyond the XCD's L2
+// on this part).
 //
 // Kernels:
-//   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row; zeroes
-//                       the dQ accumulator rows it covers (atomic path).  Both
+//   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row.  Both
 //                       statistics live in one array [B*H][2][Sq]
 //                       (LSE*log2(e) first, rowdot second), so a lane
 //                       addresses either with a 32-bit offset from a
 //                       per-head base.
-//   bwd_main_kernel     head_dim 64: workgroup = 128 keys (32 per wave) of one
-//                       KV head; loops over the 64-row query tiles of every
-//                       query head that shares the KV head (GQA).  K and V of
-//                       the wave stay in registers.
-//   bwd_main_mfma_kernel  head_dim 128 / 256 variant (fa_bwd_mfma.h).
-//   bwd_dq_kernel       query-stationary dQ (fa_bwd_dq.h).
-//   bwd_dq_convert      dQ = scale * acc, cast to the input dtype.
+//   bwd_main_kernel     head_dim 64 dK / dV: workgroup = 128 keys (32 per
+//                       wave) of one KV head; loops over the 64-row query
+//                       tiles of every query head that shares the KV head
+//                       (GQA).  K and V of the wave stay in registers.
+//   bwd_main_mfma_kernel  head_dim 128 / 256 dK / dV (fa_bwd_mfma.h).
+//   bwd_dq_kernel       dQ (fa_bwd_dq.h).
 #include "fa_bwd_dq.h"
 #include "fa_bwd_mfma.h"
 #include "fa_common.h"
@@ -67,8 +63,7 @@ template <int D>
 constexpr int pre_rows_per_block() { return 256 / (D / 8) * kPreRows; }
 
 template <class T, int D>
-__global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqacc,
-                                                      float* stats) {
+__global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* stats) {
   constexpr int LPR = D / 8;     // lanes per row
   constexpr int RPP = 256 / LPR;  // rows per pass of the block
   const int Sq = a.seqlen_q, H = a.num_heads;
@@ -101,11 +96,6 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* dqac
 #pragma unroll
     for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
     if (q < Sq) {
-      if (dqacc) {  // atomic path: the dQ accumulator starts at zero
-        float* z = dqacc + (row0 + q) * D + 8 * sub;
-        st16(z, u32x4{0, 0, 0, 0});
-        st16(z + 4, u32x4{0, 0, 0, 0});
-      }
       if (sub == 0) {
         const float l = a.lse[row0 + q];
         float* st = stats + 2 * row0 + q;
@@ -338,83 +328,28 @@ __global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const f
   }
 }
 
-// ------------------------------------------------------------ dQ convert
-// Same row order and lane split as bwd_pre_kernel: reads of the accumulator
-// are contiguous.
-template <class T, int D>
-__global__ __launch_bounds__(256) void bwd_dq_convert_kernel(fa_bwd_args a,
-                                                             const float* dqacc) {
-  constexpr int LPR = D / 8;
-  constexpr int RPP = 256 / LPR;
-  const int Sq = a.seqlen_q, H = a.num_heads;
-  const int bh = blockIdx.y;
-  const int h = bh % H, b = bh / H;
-  const int q0 = blockIdx.x * pre_rows_per_block<D>() + threadIdx.x / LPR;
-  const int sub = threadIdx.x % LPR;
-  const int64_t row0 = (int64_t)bh * Sq;
-  f32x4 x0[kPreRows], x1[kPreRows];
-#pragma unroll
-  for (int p = 0; p < kPreRows; ++p) {
-    const int q = q0 + p * RPP;
-    if (q < Sq) {
-      const float* src = dqacc + (row0 + q) * D + 8 * sub;
-      x0[p] = *reinterpret_cast<const f32x4*>(src);
-      x1[p] = *reinterpret_cast<const f32x4*>(src + 4);
-    }
-  }
-  const float sc = a.softmax_scale;
-#pragma unroll
-  for (int p = 0; p < kPreRows; ++p) {
-    const int q = q0 + p * RPP;
-    if (q >= Sq) continue;
-    u32x4 w;
-    w[0] = T::pack(x0[p][0] * sc, x0[p][1] * sc);
-    w[1] = T::pack(x0[p][2] * sc, x0[p][3] * sc);
-    w[2] = T::pack(x1[p][0] * sc, x1[p][1] * sc);
-    w[3] = T::pack(x1[p][2] * sc, x1[p][3] * sc);
-    uint16_t* dst = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] +
-                    (int64_t)q * a.dq_stride[1] + h * a.dq_stride[2] + 8 * sub;
-    st16(dst, w);
-  }
-}
-
 // ----------------------------------------------------------------- launchers
 
-// dQ by fp32 atomics (head_dim 256 unless `deterministic`) or by the
-// query-stationary kernel.
-static bool bwd_atomic_dq(const fa_bwd_args& a) {
-  return !a.deterministic && a.head_dim >= tiles::kBwdAtomicMinHeadDim;
-}
-
-// Workspace: the fp32 dQ accumulator [B, H, Sq, D] (atomic path only), then
-// the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot).
+// Workspace: the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot).
 size_t bwd_workspace_bytes(const fa_bwd_args& a) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
-  const size_t acc = bwd_atomic_dq(a) ? rows * a.head_dim * sizeof(float) : 0;
-  return acc + 2 * rows * sizeof(float) + 256;
+  return 2 * rows * sizeof(float) + 256;
 }
 
-// Key-stationary main kernel for one mask mode; DQ selects the atomic dQ
-// (head_dim 256 only).
-template <class T, int D, bool DQ>
-static void launch_bwd_main(const fa_bwd_args& a, int mode, float* dqacc, const float* stats,
-                            hipStream_t st) {
-  static_assert(!DQ || D >= tiles::kBwdAtomicMinHeadDim, "atomic dQ path");
+// Key-stationary dK / dV kernel for one mask mode.
+template <class T, int D>
+static void launch_bwd_main(const fa_bwd_args& a, int mode, const float* stats, hipStream_t st) {
   if constexpr (D >= 128) {
-    constexpr int KB = D == 128 ? kBwdKB : 1;
-    using S2 = BwdShapeMfma<D, KB>;
-    const int kvtiles = (a.seqlen_k + S2::BKV - 1) / S2::BKV;
-    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S2::NW);
-    if (kvtiles == 0) return;  // no keys: dQ stays zero; dK / dV are empty
+    using S = BwdShapeMfma<D>;
+    const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
+    const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S::NW);
+    if (kvtiles == 0) return;  // no keys: dK / dV are empty
     if (mode == kMaskCausal)
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal, KB, DQ>), grid, block, 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal>), grid, block, 0, st, a, stats);
     else if (mode == kMaskBand)
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand, KB, DQ>), grid, block, 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand>), grid, block, 0, st, a, stats);
     else
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone, KB, DQ>), grid, block, 0, st, a,
-                         dqacc, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
   } else {
     using S = BwdShape<D>;
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
@@ -429,7 +364,7 @@ static void launch_bwd_main(const fa_bwd_args& a, int mode, float* dqacc, const 
   }
 }
 
-// Query-stationary dQ kernel (deterministic path).
+// Query-stationary dQ kernel.
 template <class T, int D>
 static void launch_bwd_dq(const fa_bwd_args& a, int mode, const float* stats, hipStream_t st) {
   using S = BwdDqShape<D>;
@@ -443,34 +378,18 @@ static void launch_bwd_dq(const fa_bwd_args& a, int mode, const float* stats, hi
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
 }
 
-// Atomic-free path: pre (statistics), main without dQ, then the
-// query-stationary dQ kernel, which writes dQ directly; every output element
-// is produced by one fixed sequence of operations.  Atomic path (head_dim 256
-// unless `deterministic`): pre (statistics, zeroed accumulator), main with
-// fp32 dQ atomics, dQ convert.
+// pre (statistics), dK / dV, dQ.  Every output element is produced by one
+// fixed sequence of operations.
 template <class T, int D>
 static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
-  const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
-  constexpr bool kCanAtomic = D >= tiles::kBwdAtomicMinHeadDim;
-  const bool atomic = kCanAtomic && bwd_atomic_dq(a);
-  float* dqacc = atomic ? static_cast<float*>(ws) : nullptr;
-  float* stats = static_cast<float*>(ws) + (atomic ? rows * D : 0);  // [B*H][2][Sq]
+  float* stats = static_cast<float*>(ws);  // [B*H][2][Sq]
   const dim3 rgrid((unsigned)((a.seqlen_q + pre_rows_per_block<D>() - 1) / pre_rows_per_block<D>()),
                    (unsigned)(a.batch * a.num_heads));
-  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc, stats);
+  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int mode = mask_mode(a);
-  if constexpr (kCanAtomic) {
-    if (atomic) {
-      launch_bwd_main<T, D, true>(a, mode, dqacc, stats, st);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL((bwd_dq_convert_kernel<T, D>), rgrid, dim3(256), 0, st, a, dqacc);
-      return hipGetLastError();
-    }
-  }
-  launch_bwd_main<T, D, false>(a, mode, nullptr, stats, st);
+  launch_bwd_main<T, D>(a, mode, stats, st);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_bwd_dq<T, D>(a, mode, stats, st);

@@ -1,12 +1,10 @@
-// Deterministic dQ of the dense attention backward (head_dim 64 / 128 / 256).
+// dQ of the dense attention backward (head_dim 64 / 128 / 256).
 //
 // Replaces the reference's query-stationary dQ kernel
 // (tilelang_fa_v100/_kernels_backward.py:10-85): every dQ row is built by one
 // wave over all keys its query sees and written once, so the result does not
-// depend on the order in which workgroups run (no atomics).  Used with the
-// key-stationary dK / dV kernel compiled without its dQ products
-// (bwd_main_mfma_kernel<..., false>), this is the backward's deterministic
-// path; the default path folds dQ into that kernel with fp32 atomics.
+// depend on the order in which workgroups run (no atomics).  The key-
+// stationary kernels (bwd_main_kernel, bwd_main_mfma_kernel) compute dK / dV.
 //
 // Per 32-query-row wave and BN-key tile, with the same register layout as
 // the forward's Oᵀ = Vᵀ Pᵀ (fa_fwd_d128.h), so that no score leaves the

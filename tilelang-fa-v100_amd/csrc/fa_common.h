@@ -325,7 +325,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // issued from inline assembly.  The compiler treats every LDS access after a
 // DMA it knows of as possibly aliasing the DMA target unless it can prove
 // otherwise, and then waits for vmcnt(0) - which also waits for every
-// outstanding global atomic.  With these forms the caller owns the wait:
+// other outstanding global load.  With these forms the caller owns the wait:
 // wait_vmem() before any wave reads the target (followed by a barrier when
 // other waves read it).  M0 (the LDS base of the DMA) is a register the
 // compiler reserves, so the statements save it and put it back.
@@ -354,11 +354,6 @@ __device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_bl
       : "=&s"(saved)
       : "v"(src), "s"(lds_addr(lds_block))
       : "memory");
-}
-// Atomic fp32 add at base + voff + soff (no return value).
-__device__ __forceinline__ void buffer_atomic_add(rsrc_t r, uint32_t voff, uint32_t soff,
-                                                  float v) {
-  __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, voff, soff, 0);
 }
 
 // Workgroup order for a grid of ntiles x nbh tiles (nbh = batch x heads).

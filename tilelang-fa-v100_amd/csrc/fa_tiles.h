@@ -48,29 +48,26 @@ constexpr int kFwdCoreRows = 128;
 constexpr int kFwdCoreTileElems = 8192;  // keys x head_dim per K tile (D <= 256)
 constexpr int kFwdCoreKeys512 = 32;
 
-// ---- backward main kernel, head_dim 128 / 256 (fa_bwd_mfma.h)
+// ---- backward dK / dV kernel, head_dim 128 / 256 (fa_bwd_mfma.h)
 // KV-stationary: head_dim 128 keeps 256 keys per workgroup (8 waves x 32 keys,
 // dK / dV of a wave's 32 keys in 128 registers), head_dim 256 keeps 128 keys
-// (4 waves); 32 query rows per iteration.
-// Evidence: the dQ atomics cost 0.36-0.44 ms of T1's 1.78 ms backward and their
-// count is inverse to the keys per workgroup, so the largest key tile whose
-// dK / dV fit the register file wins; 4 waves x 64 keys (512 registers each)
-// measured slower (accumulator traffic); MFMA busy 38.1% on T1.
-constexpr int kBwd128KeyBlocksPerWave = 1;
+// (4 waves); 32 query rows per iteration.  Evidence: every Q / dO tile read
+// from LDS serves the whole key tile, so the largest key tile whose dK / dV fit
+// the register file wins; 4 waves x 64 keys (512 registers each) measured
+// 2.31 ms against 1.81 ms (T1 backward), and a two-group ping-pong schedule
+// with three Q / dO buffers 1.115 against 1.105 ms for the kernel (it runs
+// near the LDS read rate: five 1 KB operand reads per four MFMAs).
 constexpr int kBwdQueryRows = 32;
 
-// ---- backward: how dQ is reduced over key tiles (fa_bwd.hip).  head_dim
-// below kBwdAtomicMinHeadDim always takes the atomic-free path (query-
-// stationary dQ kernel); at and above it, fp32 atomics unless deterministic.
-// Evidence (fa_bwd per call, ms, atomic / atomic-free, fp16, one process):
-// D=64 B4 S2048 H16 causal 0.405 / 0.343, full 0.523 / 0.443; D=128 C2 causal
-// 0.314 / 0.300, full 0.521 / 0.507, T1 1.811 / 1.814, GQA 32/8 B2 S4096
-// causal 1.283 / 1.224, full 1.733 / 1.772, B1 S16384 H8 1.767 / 1.777, B8
-// S1024 0.203 / 0.208; D=256 B2 S8192 H8 causal 3.471 / 3.562, B2 S4096 full
-// 1.667 / 1.751.  (The atomic kernel's dQ updates are performed beyond the
-// XCD's L2 on this part and cost ~64 address cycles per instruction, a floor
-// of ~1.17 ms for T1's backward.)
-constexpr int kBwdAtomicMinHeadDim = 256;
+// ---- backward: dQ (fa_bwd_dq.h), query-stationary, no atomics.  Evidence
+// (fa_bwd per call, ms, dQ by fp32 atomics from the key-stationary kernel /
+// query-stationary kernel, fp16): D=64 B4 S2048 H16 causal 0.405 / 0.343,
+// full 0.523 / 0.443; D=128 C2 causal 0.314 / 0.300, full 0.521 / 0.507, T1
+// 1.811 / 1.814, GQA 32/8 B2 S4096 causal 1.283 / 1.224, full 1.733 / 1.772,
+// B1 S16384 H8 1.767 / 1.777, B8 S1024 0.203 / 0.208; D=256 B2 S8192 H8 causal
+// 3.474 / 2.409 (with fa_bwd.hip compiled for VGPR-form MFMA, see build.py).
+// The atomics are performed beyond the XCD's L2 on this part, ~64 address
+// cycles per instruction, a floor of ~1.17 ms for T1's backward.
 
 // ---- backward main kernel, head_dim 64 (fa_bwd.hip)
 // 128 keys per workgroup, 64 query rows per iteration, 4 waves.
