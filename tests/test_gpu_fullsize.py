@@ -9,7 +9,11 @@
   GPU, copied to the host and the oracle gathers every sequence's pages
   itself.
 * T1 (dense causal, B = 2, S = 8192, H = 16, D = 128, fp16): forward and
-  backward on the GPU; sampled (batch, head) slices against the oracle.
+  backward on the GPU; sampled (batch, head) slices against the oracle.  The
+  same at head_dim 256 (H = 8, the bench's T1-shape D = 256 point): its
+  backward runs ~2000 query tiles per key tile, far more than the small
+  shapes of test_gpu_dense.py (a build whose register allocator spilled
+  the dV accumulators got dV wrong only at this size).
 
 The GPU runs once per workload (module-scoped fixtures); the oracle checks
 are split into chunks of sequences / heads so that each test stays short.
@@ -166,6 +170,35 @@ def test_t1_slices_vs_oracle(t1, bh):
     r_out, r_lse = ref.dense_attention(sl(q), sl(k), sl(v), causal=True)
     assert_close(sl(got["out"]), r_out, what="out")
     assert_lse(got["lse"][b:b + 1, h:h + 1], r_lse)
+    r_dq, r_dk, r_dv = ref.dense_attention_backward(sl(q), sl(k), sl(v), sl(do), causal=True)
+    for name, want in (("dq", r_dq), ("dk", r_dk), ("dv", r_dv)):
+        assert_close(sl(got[name]), want, what=name)
+        assert rel_l2(sl(got[name]), want) < 1e-2, name
+
+
+@pytest.fixture(scope="module")
+def t1_d256():
+    B, S, H, D = 2, 8192, 8, 256
+    g = torch.Generator().manual_seed(1)
+    q, k, v, do = (randn(g, B, S, H, D) for _ in range(4))
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = fa.tilelang_flash_attn_func(qd, kd, vd, causal=True)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    got = dict(out=out.detach().cpu(), dq=qd.grad.cpu(), dk=kd.grad.cpu(), dv=vd.grad.cpu())
+    return (q, k, v, do), got
+
+
+T1_D256_SLICES = [(0, 0), (1, 7)]
+
+
+@pytest.mark.parametrize("bh", T1_D256_SLICES, ids=[f"b{b}h{h}" for b, h in T1_D256_SLICES])
+def test_t1_shape_d256_slices_vs_oracle(t1_d256, bh):
+    (q, k, v, do), got = t1_d256
+    b, h = bh
+    sl = lambda t: t[b:b + 1, :, h:h + 1]  # noqa: E731
+    r_out, _ = ref.dense_attention(sl(q), sl(k), sl(v), causal=True)
+    assert_close(sl(got["out"]), r_out, what="out")
     r_dq, r_dk, r_dv = ref.dense_attention_backward(sl(q), sl(k), sl(v), sl(do), causal=True)
     for name, want in (("dq", r_dq), ("dk", r_dk), ("dv", r_dv)):
         assert_close(sl(got[name]), want, what=name)

@@ -13,10 +13,11 @@
 // measured slower at every head_dim: they are performed beyond the XCD's L2
 // on this part).
 //
-// Kernels:
-//   bwd_pre_kernel      rowdot(O, dO) and LSE*log2(e) per query row.  Both
-//                       statistics live in one array [B*H][2][Sq]
-//                       (LSE*log2(e) first, rowdot second), so a lane
+// Kernels, in launch order:
+//   bwd_dq_kernel       dQ (fa_bwd_dq.h); also writes the row statistics
+//                       rowdot(O, dO) and LSE*log2(e) of the rows it owns
+//                       into one array [B*H][2][Sq] (LSE*log2(e) first,
+//                       rowdot second), so a lane of the dK / dV kernels
 //                       addresses either with a 32-bit offset from a
 //                       per-head base.
 //   bwd_main_kernel     head_dim 64 dK / dV: workgroup = 128 keys (32 per
@@ -24,7 +25,6 @@
 //                       tiles of every query head that shares the KV head
 //                       (GQA).  K and V of the wave stay in registers.
 //   bwd_main_mfma_kernel  head_dim 128 / 256 dK / dV (fa_bwd_mfma.h).
-//   bwd_dq_kernel       dQ (fa_bwd_dq.h).
 #include "fa_bwd_dq.h"
 #include "fa_bwd_mfma.h"
 #include "fa_common.h"
@@ -50,62 +50,6 @@ struct BwdShape {
   static constexpr int LDS_ELEMS = OFF_DOT + D * TS;
   static_assert(RG == 2 || RG == 4, "row grouping");
 };
-
-// ------------------------------------------------------------ preprocess
-// Grid (query blocks, B*H): block (x, bh) covers rows q = kPreRowsPerBlock x
-// .. +kPreRowsPerBlock-1 of (batch, head) bh, so the statistics and the dQ
-// accumulator ([B, H, Sq, D]) are written contiguously and no lane divides.
-// LPR lanes (16 bytes of O and dO each) per row, kPreRows rows per lane
-// group, all loads issued first.
-constexpr int kPreRows = tiles::kBwdPreRows;
-
-template <int D>
-constexpr int pre_rows_per_block() { return 256 / (D / 8) * kPreRows; }
-
-template <class T, int D>
-__global__ __launch_bounds__(256) void bwd_pre_kernel(fa_bwd_args a, float* stats) {
-  constexpr int LPR = D / 8;     // lanes per row
-  constexpr int RPP = 256 / LPR;  // rows per pass of the block
-  const int Sq = a.seqlen_q, H = a.num_heads;
-  const int bh = blockIdx.y;
-  const int h = bh % H, b = bh / H;
-  const int q0 = blockIdx.x * pre_rows_per_block<D>() + threadIdx.x / LPR;
-  const int sub = threadIdx.x % LPR;
-  const uint16_t* ob = static_cast<const uint16_t*>(a.out) + b * a.o_stride[0] +
-                       h * a.o_stride[2] + 8 * sub;
-  const uint16_t* db = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
-                       h * a.do_stride[2] + 8 * sub;
-  u32x4 ov[kPreRows], dv[kPreRows];
-#pragma unroll
-  for (int p = 0; p < kPreRows; ++p) {
-    const int q = q0 + p * RPP;
-    ov[p] = dv[p] = u32x4{0, 0, 0, 0};
-    if (q < Sq) {
-      ov[p] = ld16(ob + (int64_t)q * a.o_stride[1]);
-      dv[p] = ld16(db + (int64_t)q * a.do_stride[1]);
-    }
-  }
-  const int64_t row0 = (int64_t)bh * Sq;
-#pragma unroll
-  for (int p = 0; p < kPreRows; ++p) {
-    const int q = q0 + p * RPP;
-    float acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      acc += T::lo(ov[p][w]) * T::lo(dv[p][w]) + T::hi(ov[p][w]) * T::hi(dv[p][w]);
-#pragma unroll
-    for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
-    if (q < Sq) {
-      if (sub == 0) {
-        const float l = a.lse[row0 + q];
-        float* st = stats + 2 * row0 + q;
-        // A row that saw no key has lse = -inf; +inf makes its P exactly zero.
-        st[0] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
-        st[Sq] = acc;
-      }
-    }
-  }
-}
 
 // ------------------------------------------------------------ main kernel
 // head_dim 64: dK / dV only (dQ comes from bwd_dq_kernel).  MODE (MaskMode):
@@ -364,9 +308,9 @@ static void launch_bwd_main(const fa_bwd_args& a, int mode, const float* stats, 
   }
 }
 
-// Query-stationary dQ kernel.
+// Query-stationary dQ kernel (also writes the row statistics).
 template <class T, int D>
-static void launch_bwd_dq(const fa_bwd_args& a, int mode, const float* stats, hipStream_t st) {
+static void launch_bwd_dq(const fa_bwd_args& a, int mode, float* stats, hipStream_t st) {
   using S = BwdDqShape<D>;
   const int qtiles = (a.seqlen_q + S::BM - 1) / S::BM;
   const dim3 grid((unsigned)qtiles * a.num_heads * a.batch), block(64 * S::NW);
@@ -378,21 +322,16 @@ static void launch_bwd_dq(const fa_bwd_args& a, int mode, const float* stats, hi
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
 }
 
-// pre (statistics), dK / dV, dQ.  Every output element is produced by one
-// fixed sequence of operations.
+// dQ (and the row statistics), then dK / dV.  Every output element is
+// produced by one fixed sequence of operations.
 template <class T, int D>
 static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
   float* stats = static_cast<float*>(ws);  // [B*H][2][Sq]
-  const dim3 rgrid((unsigned)((a.seqlen_q + pre_rows_per_block<D>() - 1) / pre_rows_per_block<D>()),
-                   (unsigned)(a.batch * a.num_heads));
-  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), rgrid, dim3(256), 0, st, a, stats);
+  const int mode = mask_mode(a);
+  launch_bwd_dq<T, D>(a, mode, stats, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int mode = mask_mode(a);
   launch_bwd_main<T, D>(a, mode, stats, st);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  launch_bwd_dq<T, D>(a, mode, stats, st);
   return hipGetLastError();
 }
 

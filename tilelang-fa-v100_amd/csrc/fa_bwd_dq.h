@@ -15,7 +15,7 @@
 //   dQᵀ += Kᵀ dSᵀ   (A = Kᵀ by ds_read_b64_tr_b16 from the same K tile,
 //                    B = dSᵀ packed straight from the accumulators)
 // A lane's scores all belong to its own query row (column lr of Sᵀ), so the
-// row statistics (LSE·log2e, rowdot from bwd_pre_kernel) are one register
+// row statistics (LSE·log2e, rowdot, computed here) are one register
 // each.  K and V tiles go HBM -> LDS with global_load_lds_dwordx4 (every
 // wave loads BPW 1 KB blocks of each, two tiles in flight), rows stored
 // with the 16-byte chunk swizzle of fa_fwd_d128.h.
@@ -46,7 +46,7 @@ struct BwdDqShape {
 
 template <class T, int D_, int MODE>
 __global__ __launch_bounds__((64 * BwdDqShape<D_>::NW), (BwdDqShape<D_>::WPE))
-void bwd_dq_kernel(fa_bwd_args a, const float* stats) {
+void bwd_dq_kernel(fa_bwd_args a, float* stats) {
   using S = BwdDqShape<D_>;
   constexpr int D = S::D, BN = S::BN;
   __shared__ __attribute__((aligned(16))) char k0[S::TILEB], v0[S::TILEB], k1[S::TILEB],
@@ -86,23 +86,41 @@ void bwd_dq_kernel(fa_bwd_args a, const float* stats) {
   const int my_lo = row_valid ? kv_lo(row) : 0;
   const int my_hi = row_valid ? kv_hi(row) : 0;
 
-  // ---- this lane's query row: Q and dO as B operands, its statistics.
+  // ---- this lane's query row: Q and dO as B operands, and its statistics,
+  // computed here and stored for the dK / dV kernel, which runs after this
+  // one: LSE·log2(e) (+inf for a row that saw no key, and for rows past Sq,
+  // so that P is exactly zero) and rowdot = Σ_d O·dO (the reference's
+  // row_dot, _kernels_backward.py:203).  Lanes l and l + 32 hold the two
+  // halves of each 16-column chunk of the row.
   u32x4 qf[D / 16], df[D / 16];
-  float lse2 = __builtin_inff(), rdot = 0.f;  // +inf: P = 0 for rows past Sq
+  float lse2 = __builtin_inff(), rdot = 0.f;
   {
+    const int64_t r = min(row, Sq - 1);
     const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] +
-                         h * a.q_stride[2] + (int64_t)min(row, Sq - 1) * a.q_stride[1];
+                         h * a.q_stride[2] + r * a.q_stride[1];
     const uint16_t* dp = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
-                         h * a.do_stride[2] + (int64_t)min(row, Sq - 1) * a.do_stride[1];
+                         h * a.do_stride[2] + r * a.do_stride[1];
+    const uint16_t* op = static_cast<const uint16_t*>(a.out) + b * a.o_stride[0] +
+                         h * a.o_stride[2] + r * a.o_stride[1];
+    float part = 0.f;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       qf[c] = ld16(qp + 16 * c + 8 * lh);
       df[c] = ld16(dp + 16 * c + 8 * lh);
+      const u32x4 ov = ld16(op + 16 * c + 8 * lh);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) part = T::dot2(ov[w], df[c][w], part);
     }
+    const float full = part + __shfl_xor(part, 32);
     if (row_valid) {
-      const float* st = stats + 2 * (int64_t)bh * Sq;
-      lse2 = st[row];
-      rdot = st[Sq + row];
+      const float l = a.lse[(int64_t)bh * Sq + row];
+      lse2 = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
+      rdot = full;
+      if (lh == 0) {
+        float* st = stats + 2 * (int64_t)bh * Sq;
+        st[row] = lse2;
+        st[Sq + row] = rdot;
+      }
     }
   }
 

@@ -69,6 +69,11 @@ struct Half {
     const f16x2 one = {(_Float16)1.f, (_Float16)1.f};
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
   }
+  // acc + lo(a) lo(b) + hi(a) hi(b): the fp16 products are exact in fp32.
+  __device__ __forceinline__ static float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc,
+                                  false);
+  }
   __device__ __forceinline__ static float lo(uint32_t w) {
     return (float)__builtin_bit_cast(f16x2, w)[0];
   }
@@ -96,6 +101,10 @@ struct BFloat16 {
   // bf16 keeps 8 significant bits: the row sum uses the fp32 values.
   __device__ __forceinline__ static float sum2(float p0, float p1, uint32_t, float acc) {
     return acc + p0 + p1;
+  }
+  // acc + lo(a) lo(b) + hi(a) hi(b) in fp32 (exact products, two roundings).
+  __device__ __forceinline__ static float dot2(uint32_t a, uint32_t b, float acc) {
+    return fmaf(hi(a), hi(b), fmaf(lo(a), lo(b), acc));
   }
   __device__ __forceinline__ static float lo(uint32_t w) {
     return __builtin_bit_cast(float, w << 16);

@@ -74,12 +74,6 @@ constexpr int kBwdQueryRows = 32;
 constexpr int kBwd64Keys = 128;
 constexpr int kBwd64QueryRows = 64;
 
-// ---- backward row kernels (fa_bwd.hip): 2 rows per lane group (D / 8
-// lanes per row) with all their loads issued together.  Evidence (C2 kernel
-// trace, pre / dQ convert, us): 1 row 28.7 / 16.9; 2 rows 26.2-26.6 /
-// 16.7-16.9; 4 rows 28.7 / 17.7; 8 rows 60.1 / 17.4.
-constexpr int kBwdPreRows = 2;
-
 // ---- decode, head_dim 64 / 128 / 256 (fa_decode_stream.h)
 // Persistent waves; work item = a split of keys x one KV head x its query
 // heads (up to 8, the 16x16x32 MFMA columns); 16-key tiles, two in flight
