@@ -27,13 +27,18 @@ SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_decode.hip", "fa_cache.hip", "fa_scra
            "fa_capi.cpp"]
 ARCH = "gfx950"
 
-# Per-source flags.  fa_bwd.hip: MFMA results in VGPRs.  Its head_dim 256
-# dK / dV kernel holds dK / dV in the 256 accumulator registers; with the
-# default heuristic the S / dP accumulators were placed there too and 32 of
-# them spilled to scratch every tile (T1-shape head_dim 256 backward 3.54 ms,
-# 2.41 ms in this form).  The head_dim 64 / 128 kernels compile to the same
-# code either way.
-SOURCE_FLAGS = {"fa_bwd.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+# Per-source flags: MFMA results in VGPRs (the "VGPR form"; AGPRs then hold
+# what does not fit).  fa_bwd.hip: its head_dim 256 dK / dV kernel holds
+# dK / dV in the 256 accumulator registers; with the default heuristic the
+# S / dP accumulators were placed there too and 32 of them spilled to scratch
+# every tile (T1-shape head_dim 256 backward 3.54 ms, 2.41 ms in this form).
+# fa_fwd.hip: the generic core at head_dim 512 spilled 35 VGPRs (none in this
+# form; paged prefill 3.96 -> 3.60 ms) and at head_dim 256 with small pages
+# ran 9% faster.  Every head_dim 64 / 128 kernel, and the head_dim 256 cores
+# that keep their accumulators in VGPRs anyway, compile to the same code
+# either way.
+_VGPR_FORM = ["-mllvm", "--amdgpu-mfma-vgpr-form"]
+SOURCE_FLAGS = {"fa_bwd.hip": _VGPR_FORM, "fa_fwd.hip": _VGPR_FORM}
 
 COMMON_FLAGS = [
     "-O3",

@@ -412,12 +412,23 @@ static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
   const int mode = mask_mode(a);
-  if (mode == kMaskCausal)
-    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskCausal>), grid, dim3(C::THREADS), 0, st, a);
-  else if (mode == kMaskBand)
+  if constexpr (D == 256 && T::kId == FA_DTYPE_BF16) {
+    // bf16 at head_dim 256: the band instance (band from the arguments; causal
+    // and full attention are bands too) for every mode.  The causal and
+    // full instances spilled 190 VGPRs in the loop (the fp32 row sum of
+    // bf16 keeps more values live than fp16's packed-word sum, and the
+    // register allocator lost the two-waves-per-SIMD budget); the band
+    // instance fits 230 without spills.
+    (void)mode;
     hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskBand>), grid, dim3(C::THREADS), 0, st, a);
-  else
-    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskNone>), grid, dim3(C::THREADS), 0, st, a);
+  } else {
+    if (mode == kMaskCausal)
+      hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskCausal>), grid, dim3(C::THREADS), 0, st, a);
+    else if (mode == kMaskBand)
+      hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskBand>), grid, dim3(C::THREADS), 0, st, a);
+    else
+      hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskNone>), grid, dim3(C::THREADS), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -42,7 +42,8 @@ constexpr int kFwd256Waves = 8;
 // 512 registers; 2 waves per SIMD for D <= 128, 1 above.
 // Evidence (compiler resource usage): D = 64 takes 182 VGPRs and D = 256
 // 254 VGPRs + 152 AGPRs (one wave per SIMD), both without spills; D = 512
-// (two O passes) 512 registers with 35 spilled.  C1 (D = 64) is launch-bound
+// (two O passes) 253 VGPRs + 160 AGPRs in the VGPR MFMA form fa_fwd.hip is
+// built in (35 spilled in the default form).  C1 (D = 64) is launch-bound
 // (13.5 us), so its tile is sized for occupancy, not peak rate.
 constexpr int kFwdCoreRows = 128;
 constexpr int kFwdCoreTileElems = 8192;  // keys x head_dim per K tile (D <= 256)
