@@ -164,8 +164,8 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
       const int r = S::RPB * blk + lane / S::CPR;
       const int c = (lane % S::CPR) ^ swz(r);
       const int n = min(n0 + r, ld_last);
-      load_lds16(kg + (int64_t)n * a.k_stride[1] + 8 * c, kb + blk * 1024);
-      load_lds16(vg + (int64_t)n * a.v_stride[1] + 8 * c, vb + blk * 1024);
+      global_lds16_opaque(kg + (int64_t)n * a.k_stride[1] + 8 * c, kb + blk * 1024);
+      global_lds16_opaque(vg + (int64_t)n * a.v_stride[1] + 8 * c, vb + blk * 1024);
     }
   };
 
@@ -176,28 +176,41 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
     const bool need_mask = (n0 < w_lo_max) || (n0 + BN > w_hi_min);
 #pragma unroll
     for (int kt = 0; kt < BN / 32; ++kt) {
+      // Sᵀ first; then each dPᵀ product is followed by 16 / (D / 16)
+      // elements of P, so the exponentials issue while the matrix core works
+      // through dPᵀ (the two chains interleaved left them to run after both).
+      const int ko = kt * 32 * S::ROWB;
       f32x16 s, dp;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
-      const int ko = kt * 32 * S::ROWB;
+      for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        s = T::mma32(ld16(kb + koff[c] + ko), qf[c], s);
-        dp = T::mma32(ld16(vb + koff[c] + ko), df[c], dp);
-      }
-      sched_pipeline<D / 16, 2, 2, 2>();
+      for (int c = 0; c < D / 16; ++c) s = T::mma32(ld16(kb + koff[c] + ko), qf[c], s);
+      sched_pipeline<D / 16, 1, 1, 2>();
       // P and dS; element i is key n0 + 32kt + 8(i/4) + 4lh + i%4.
       auto probs = [&](auto masked) {
         constexpr bool kMasked = decltype(masked)::value;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 16; ++i) dp[i] = 0.f;
+        auto prob = [&](int i) {
           float p = fast_exp2(fmaf(s[i], scale_log2, -lse2));
           if constexpr (kMasked) {
             const int kv = n0 + kt * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
             p = (kv >= my_lo && kv < my_hi) ? p : 0.f;
           }
-          dp[i] = p * (dp[i] - rdot);
-        }
+          s[i] = p;
+        };
+        constexpr int EPC = 16 / (D / 16) > 0 ? 16 / (D / 16) : 1;
+        lds_pipeline<D / 16, 2>([&](int c) { return ld16(vb + koff[c] + ko); },
+                                [&](int c, const u32x4& av) {
+                                  dp = T::mma32(av, df[c], dp);
+#pragma unroll
+                                  for (int e = 0; e < EPC; ++e)
+                                    if (EPC * c + e < 16) prob(EPC * c + e);
+                                });
+#pragma unroll
+        for (int i = EPC * (D / 16); i < 16; ++i) prob(i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dp[i] = s[i] * (dp[i] - rdot);
       };
       if (need_mask)
         probs(BoolC<true>{});

@@ -94,7 +94,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
     const int r = S::RPB * blk + lane / S::CPR;
     const int c = (lane % S::CPR) ^ swz_chunk(r);
     const int n = min(kv0 + r, Sk - 1);
-    load_lds16(kg + (int64_t)n * a.k_stride[1] + 8 * c, Ks + blk * 1024);
+    global_lds16_opaque(kg + (int64_t)n * a.k_stride[1] + 8 * c, Ks + blk * 1024);
   }
   // ---- V rows of this wave (B operand of dP = dO Vᵀ)
   u32x4 vB[D / 16];

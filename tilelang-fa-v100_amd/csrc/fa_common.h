@@ -365,6 +365,25 @@ __device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_bl
       : "memory");
 }
 
+// 16 bytes per lane from src into LDS (lane l writes lds_block + 16l), as an
+// opaque global_load_lds_dwordx4 (same contract as global_lds4_opaque).  With
+// the compiler-visible form the waitcnt pass counted every later LDS read
+// against the DMA and waited for lgkmcnt(0) before each product, so operand
+// reads issued ahead of a product gave no overlap.
+__device__ __forceinline__ void global_lds16_opaque(const void* src, void* lds_block) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_addr(lds_block))
+      : "memory");
+}
+
 // Workgroup order for a grid of ntiles x nbh tiles (nbh = batch x heads).
 // The hardware hands workgroup ids to the 8 XCDs round-robin and each XCD
 // starts its ids in increasing order.  Each XCD is given a contiguous block

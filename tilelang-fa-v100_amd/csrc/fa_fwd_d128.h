@@ -48,10 +48,6 @@ __device__ __forceinline__ u32x2 lds_read_tr(const char* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lp));
 }
 
-__device__ __forceinline__ void load_lds16(const void* g, char* lds_block) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
-}
-
 // Waits for this wave's outstanding global loads (including those that
 // write LDS directly): vmcnt(0), expcnt/lgkmcnt untouched.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -143,8 +139,8 @@ __device__ __forceinline__ void attn_fwd_tile_d128_plain(const Prob& P, int row0
       const int r = 4 * blk + (lane >> 4);
       const int c = (lane & 15) ^ swz_chunk(r);
       const int n = min(n0 + r, ld_last);
-      load_lds16(P.k_ptr(n) + 8 * c, kb + blk * 1024);
-      load_lds16(P.v_ptr(n) + 8 * c, vb + blk * 1024);
+      global_lds16_opaque(P.k_ptr(n) + 8 * c, kb + blk * 1024);
+      global_lds16_opaque(P.v_ptr(n) + 8 * c, vb + blk * 1024);
     }
   };
 
