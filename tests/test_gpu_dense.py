@@ -57,6 +57,38 @@ def test_forward_matches_oracle(case):
     assert rel_l2(out, r_out) < 1e-2
 
 
+# More row tiles than the GPU holds workgroups at once, so each workgroup of
+# the forward runs several of them in a row (rounds of its persistent
+# schedule): batch x heads not a multiple of 8 (the schedule's fallback
+# order), GQA, windows, full attention, and the 4-wave head_dim 64 core (two
+# workgroups per CU).  The oracle checks sampled (batch, head) slices.
+MANY_TILE_CASES = [
+    # (B, S, H, Hk, D, causal, window, dtype)
+    (3, 8192, 5, 5, 128, True, (-1, -1), torch.float16),
+    (1, 8192, 12, 4, 128, True, (300, -1), torch.bfloat16),
+    (2, 4096, 24, 8, 256, False, (-1, -1), torch.float16),
+    (1, 8192, 9, 3, 64, True, (-1, -1), torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", MANY_TILE_CASES,
+                         ids=[f"B{c[0]}-S{c[1]}-H{c[2]}/{c[3]}-D{c[4]}-{'c' if c[5] else 'nc'}"
+                              f"-w{c[6][0]}-{str(c[7])[6:]}" for c in MANY_TILE_CASES])
+def test_forward_with_several_tiles_per_workgroup(case):
+    B, S, H, Hk, D, causal, window, dt = case
+    g = torch.Generator(device=DEV).manual_seed(11)
+    q, k, v = (torch.randn(B, S, h, D, device=DEV, generator=g).to(dt) for h in (H, Hk, Hk))
+    out, lse, _ = fa.tilelang_flash_attn_func(q, k, v, causal=causal, window_size=window,
+                                              return_attn_probs=True)
+    G = H // Hk
+    for b, h in ((B - 1, 0), (B - 1, H - 1), (0, H // 2)):
+        sl = lambda t, hh: t[b:b + 1, :, hh:hh + 1].cpu()
+        r_out, r_lse = ref.dense_attention(sl(q, h), sl(k, h // G), sl(v, h // G), causal=causal,
+                                           window=window)
+        assert_close(out[b:b + 1, :, h:h + 1], r_out, what=f"out b{b} h{h}")
+        assert_lse(lse[b:b + 1, h:h + 1], r_lse)
+
+
 def test_forward_peaky_scores_and_custom_scale():
     g = torch.Generator().manual_seed(1)
     q = randn(g, 2, 384, 8, 128, scale=4.0)

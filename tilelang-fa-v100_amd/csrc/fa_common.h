@@ -405,6 +405,40 @@ __device__ __forceinline__ TileHead xcd_tile_order(int wg, int ntiles, int nbh) 
   return {wg / nbh, wg % nbh};
 }
 
+// Persistent schedule over the virtual workgroup ids of xcd_tile_order: a
+// grid of W workgroups (as many as fit the GPU at once) walks total =
+// ntiles x nbh tiles, workgroup w taking one tile per round r.  Within a
+// round the tiles go out in xcd_tile_order's order (heaviest causal rank
+// first), and the direction alternates between rounds (the heaviest tile of
+// one round pairs with the lightest of the next), which balances the
+// per-workgroup sums of linearly decreasing tile costs.  When nbh is a
+// multiple of 8 (then W is too), workgroup w stays on its XCD's heads: it
+// runs on XCD w % 8 and takes virtual ids 8 local + w % 8.  Returns the
+// virtual id, or -1 when workgroup w has no tile in round r (nor in any
+// later round).
+__device__ __forceinline__ int persistent_tile(int w, int W, int r, int total, int nbh) {
+  constexpr int kXcds = 8;
+  if (nbh % kXcds == 0) {
+    const int wx = W / kXcds, l = w / kXcds;
+    const int local = r * wx + ((r & 1) ? wx - 1 - l : l);
+    return local < total / kXcds ? local * kXcds + w % kXcds : -1;
+  }
+  const int v = r * W + ((r & 1) ? W - 1 - w : w);
+  return v < total ? v : -1;
+}
+
+// The kernel's arguments, read through a pointer the compiler cannot
+// follow, so each use reloads them from the kernarg segment (scalar loads)
+// instead of keeping every field in scalar registers for the kernel's whole
+// life: a persistent loop that sets up each tile from them would otherwise
+// spill.
+template <class Args>
+__device__ __forceinline__ const __attribute__((address_space(4))) Args* kernel_args() {
+  auto p = (const __attribute__((address_space(4))) Args*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
 // XCD-aware workgroup order.  The hardware hands consecutive workgroup ids to
 // the 8 XCDs round-robin; remapping makes each XCD receive a contiguous range
 // of logical tiles, so tiles that share K/V rows share one L2.

@@ -55,6 +55,7 @@ struct FwdKernelCfg {
   static constexpr int BM = FwdShape<D>::BM;
   static constexpr int THREADS = 256;
   static constexpr int WAVES_PER_EU = FwdShape<D>::kWavesPerEU;
+  static constexpr int WG_PER_CU = WAVES_PER_EU;  // 4 waves: one per SIMD each
   static constexpr int LDS_BYTES = FwdShape<D>::LDS_ELEMS * 2;
 };
 template <>
@@ -62,6 +63,7 @@ struct FwdKernelCfg<256, true> {
   static constexpr int BM = FwdShapeD256::BM;
   static constexpr int THREADS = 512;
   static constexpr int WAVES_PER_EU = 2;
+  static constexpr int WG_PER_CU = 1;
   static constexpr int LDS_BYTES = FwdShapeD256::LDS_BYTES;
 };
 template <bool PP>
@@ -69,6 +71,7 @@ struct FwdKernelCfg<128, PP> {
   static constexpr int BM = FwdShapeD128::BM;
   static constexpr int THREADS = 512;
   static constexpr int WAVES_PER_EU = 2;
+  static constexpr int WG_PER_CU = 1;
   static constexpr int LDS_BYTES = FwdShapeD128::LDS_BYTES;
 };
 
@@ -97,6 +100,27 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
   }
 }
 
+// A sequence of row tiles on one workgroup: next(P, row0) rewrites the
+// problem and first row for the next tile, false after the last one.  The
+// D = 128 ping-pong core overlaps each tile's output stores with the next
+// tile's first loads; the other cores run the tiles one after the other,
+// with a barrier between them (their last LDS reads are not followed by a
+// barrier of their own).
+template <class T, int D, bool PP, class Prob, class Next>
+__device__ __forceinline__ void run_fwd_tiles(Prob P, int row0, float scale, Next next) {
+  if constexpr (D == 128 && PP) {
+    constexpr int B = FwdShapeD128::LDS_ARRAY_BYTES;
+    __shared__ __attribute__((aligned(16))) char k0[B], v0[B], k1[B], v1[B];
+    attn_fwd_tiles_d128<T>(P, row0, scale, k0, v0, k1, v1, next);
+  } else {
+    for (;;) {
+      run_fwd_tile<T, D, PP>(P, row0, scale);
+      if (!next(P, row0)) break;
+      __syncthreads();
+    }
+  }
+}
+
 // MODE (MaskMode): full attention, causal, or a window band from the
 // arguments.  The causal and full bands are compile-time constants.
 template <class T, int D, int MODE>
@@ -105,32 +129,50 @@ __global__ __launch_bounds__((FwdKernelCfg<D, true>::THREADS),
 void fwd_dense_kernel(fa_fwd_args a) {
   using C = FwdKernelCfg<D, true>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
-  const TileHead th = xcd_tile_order(blockIdx.x, qtiles, a.batch * a.num_heads);
-  const int bh = th.bh;
-  const int h = bh % a.num_heads;
-  const int b = bh / a.num_heads;
-  // Heaviest causal tiles (largest query index) first.
-  const int qt = MODE != kMaskNone ? qtiles - 1 - th.rank : th.rank;
-  const int hk = h / (a.num_heads / a.num_heads_k);
-
+  const int nbh = a.batch * a.num_heads;
+  // Persistent: this workgroup's tiles are rounds 0, 1, ... of
+  // persistent_tile (one workgroup per tile when the grid covers them all).
+  // Each tile's problem is set up from the arguments in the kernarg segment.
+  auto setup = [qtiles, nbh](int vid, DenseRows& P, int& row0) {
+    const auto* ap = kernel_args<fa_fwd_args>();
+    const TileHead th = xcd_tile_order(vid, qtiles, nbh);
+    const int bh = th.bh;
+    const int H = ap->num_heads;
+    const int h = bh % H;
+    const int b = bh / H;
+    // Heaviest causal tiles (largest query index) first.
+    const int qt = MODE != kMaskNone ? qtiles - 1 - th.rank : th.rank;
+    const int hk = h / (H / ap->num_heads_k);
+    P.q = static_cast<const uint16_t*>(ap->q) + b * ap->q_stride[0] + h * ap->q_stride[2];
+    P.o = static_cast<uint16_t*>(ap->out) + b * ap->o_stride[0] + h * ap->o_stride[2];
+    P.lse = ap->lse ? ap->lse + ((int64_t)b * H + h) * ap->seqlen_q : nullptr;
+    P.k = static_cast<const uint16_t*>(ap->k) + b * ap->k_stride[0] + hk * ap->k_stride[2];
+    P.v = static_cast<const uint16_t*>(ap->v) + b * ap->v_stride[0] + hk * ap->v_stride[2];
+    P.qs = ap->q_stride[1];
+    P.os = ap->o_stride[1];
+    P.ks = ap->k_stride[1];
+    P.vs = ap->v_stride[1];
+    P.nrows = ap->seqlen_q;
+    P.sk = ap->seqlen_k;
+    P.off = ap->seqlen_k - ap->seqlen_q;
+    const Band band = mode_band<MODE>(*ap);
+    P.wl = band.wl;
+    P.wr = band.wr;
+    P.has_lse = ap->lse != nullptr;
+    row0 = qt * C::BM;
+  };
+  int r = 0;
+  const int vid = persistent_tile(blockIdx.x, gridDim.x, r, qtiles * nbh, nbh);
+  if (vid < 0) return;
   DenseRows P;
-  P.q = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] + h * a.q_stride[2];
-  P.o = static_cast<uint16_t*>(a.out) + b * a.o_stride[0] + h * a.o_stride[2];
-  P.lse = a.lse ? a.lse + ((int64_t)b * a.num_heads + h) * a.seqlen_q : nullptr;
-  P.k = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
-  P.v = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
-  P.qs = a.q_stride[1];
-  P.os = a.o_stride[1];
-  P.ks = a.k_stride[1];
-  P.vs = a.v_stride[1];
-  P.nrows = a.seqlen_q;
-  P.sk = a.seqlen_k;
-  P.off = a.seqlen_k - a.seqlen_q;
-  const Band band = mode_band<MODE>(a);
-  P.wl = band.wl;
-  P.wr = band.wr;
-  P.has_lse = a.lse != nullptr;
-  run_fwd_tile<T, D, true>(P, qt * C::BM, a.softmax_scale);
+  int row0 = 0;
+  setup(vid, P, row0);
+  run_fwd_tiles<T, D, true>(P, row0, a.softmax_scale, [&](DenseRows& Pn, int& rn) {
+    const int v = persistent_tile(blockIdx.x, gridDim.x, ++r, qtiles * nbh, nbh);
+    if (v < 0) return false;
+    setup(v, Pn, rn);
+    return true;
+  });
 }
 
 struct PagedRows {
@@ -410,7 +452,7 @@ template <class T, int D>
 static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   using C = FwdKernelCfg<D, true>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
-  const dim3 grid((unsigned)qtiles * a.num_heads * a.batch);
+  const dim3 grid((unsigned)persistent_grid(qtiles, a.num_heads * a.batch, C::WG_PER_CU));
   const int mode = mask_mode(a);
   if constexpr (D == 256 && T::kId == FA_DTYPE_BF16) {
     // bf16 at head_dim 256: the band instance (band from the arguments; causal

@@ -237,9 +237,17 @@ __device__ __forceinline__ void attn_fwd_tile_d128_plain(const Prob& P, int row0
 // loop is unrolled by two so that every LDS read names one array pair while
 // the DMA of the next tile targets the other; the compiler can then see that
 // the reads do not depend on the outstanding DMA and does not wait for it.
-template <class T, class Prob>
-__device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, float scale,
-                                                   char* k0, char* v0, char* k1, char* v1) {
+//
+// attn_fwd_tiles_d128 runs a sequence of row tiles on one workgroup:
+// next(P, row0) rewrites the problem and first row for the next tile and
+// returns false after the last one.  Between tiles no CU time is lost to a
+// workgroup's teardown and launch: once every wave is past a tile's last
+// barrier (LDS and the Q registers are free), the tile's output stores go
+// out, then the next tile's Q rows and first K tile are requested, and their
+// latencies overlap.
+template <class T, class Prob, class Next>
+__device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scale, char* k0,
+                                                    char* v0, char* k1, char* v1, Next next) {
   using S = FwdShapeD128;
   constexpr int D = S::D, BN = S::BN;
   const float scale_log2 = scale * kLog2e;
@@ -247,32 +255,9 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
-
-  const int nrows = P.nrows;
-  const int row_last = min(row0 + S::BM, nrows) - 1;
-  const int wg_lo = P.kv_lo(row0);
-  const int wg_hi = P.kv_hi(row_last);
-
-  const int wrow0 = row0 + wave * 32;
-  const bool wave_active = wrow0 < nrows;
-  const int wrow_last = min(wrow0 + 31, nrows - 1);
-  const int w_lo_min = wave_active ? P.kv_lo(wrow0) : 0;
-  const int w_lo_max = wave_active ? P.kv_lo(wrow_last) : 0;
-  const int w_hi_min = wave_active ? P.kv_hi(wrow0) : 0;
-  const int w_hi_max = wave_active ? P.kv_hi(wrow_last) : 0;
-
-  const int row = wrow0 + lr;
-  const bool row_valid = row < nrows;
-  const int my_lo = row_valid ? P.kv_lo(row) : 0;
-  const int my_hi = row_valid ? P.kv_hi(row) : 0;
-
-  u32x4 qf[D / 16];
-  {
-    const uint16_t* qp = row_valid ? P.q_ptr(row) : nullptr;
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c)
-      qf[c] = row_valid ? ld16(qp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
-  }
+  const bool grp_b = wave >= S::NW / 2;
+  constexpr int DB = 16 / (S::NW / 2);  // blocks per DMA wave
+  static_assert(DB * 4 == 16, "each DMA wave fills 16 rows");
 
   // ---- per-lane LDS offsets (bytes, relative to a K or V tile base)
   // K operand of Sᵀ = K Qᵀ, chunk c: row lr (+32 kt), logical chunk 2c + lh.
@@ -296,6 +281,82 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
       voff[hf][dt] = r * S::ROWB + 16 * (chunk ^ sw) + 8 * (lane & 1);
     }
   }
+
+  // K / V rows are a base plus a row stride: tiles are DMA'd through buffer
+  // resources, the lane's byte offset within the tile is fixed, the tile
+  // base is scalar, and rows at or past the last key read as zero (their
+  // scores are masked).  Group A alone issues them, from inside its matrix
+  // phase: issuing 32 KB per tile from all eight waves at the start of a
+  // slot stalled them on the vector-memory queue; behind a burst of MFMAs
+  // the queueing overlaps the matrix core's work (wave w < 4 fills 1 KB
+  // blocks 4w .. 4w+3, i.e. keys n0 + 16w .. n0 + 16w + 15).  A wave's 16
+  // rows are a base plus the row stride: for paged K / V (pages of at least
+  // 16 keys) they lie in one page, whose block-table entry is one scalar
+  // load per wave and tile.  The row strides are those of the launch, the
+  // same for every tile.
+  uint32_t k_loff[DB], v_loff[DB];
+#pragma unroll
+  for (int ii = 0; ii < DB; ++ii) {
+    const int r = 4 * (DB * wave + ii) + (lane >> 4);  // row of the tile
+    const uint32_t r16 = 4 * ii + (lane >> 4);         // row of the wave's 16
+    const uint32_t chunk = 8u * ((lane & 15) ^ swz_chunk(r));
+    k_loff[ii] = 2u * (r16 * (uint32_t)P.k_row_stride() + chunk);
+    v_loff[ii] = 2u * (r16 * (uint32_t)P.v_row_stride() + chunk);
+  }
+  // Keys n0 .. n0 + 63 of the problem (keys below wg_hi exist) into dst.
+  auto issue_rows = [&](int wg_hi, int n0, char* dst, auto is_v) {
+    constexpr bool kV = decltype(is_v)::value;
+    const int nw = n0 + 16 * wave;
+    const int nvalid = min(16, wg_hi - nw);  // n0 < wg_hi, so n0's row resolves
+    const int nb = nvalid > 0 ? nw : n0;
+    const uint16_t* base = kV ? P.v_ptr(nb) : P.k_ptr(nb);
+    // The range ends after the last valid row's D columns (not nvalid whole
+    // strides): a size-1 sequence dimension may come with stride 0.
+    const uint32_t bytes = span_bytes(nvalid, kV ? P.v_row_stride() : P.k_row_stride(), D);
+    u32x4 rs = rsrc_words(base, bytes);
+    // Uniform by construction (the block-table read of a paged problem is
+    // not known to be); the resource must sit in scalar registers.
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(rs[w]);
+#pragma unroll
+    for (int ii = 0; ii < DB; ++ii)
+      buffer_lds16_opaque(rs, kV ? v_loff[ii] : k_loff[ii], dst + (DB * wave + ii) * 1024);
+  };
+
+  // This lane's Q row of the tile (P, row0), and (group A) its first K tile
+  // into k0.
+  u32x4 qf[D / 16];
+  auto start_tile = [&]() {
+    const int rw = row0 + wave * 32 + lr;
+    const bool valid = rw < P.nrows;
+    const uint16_t* qp = valid ? P.q_ptr(rw) : nullptr;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) qf[c] = valid ? ld16(qp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
+    const int hi = P.kv_hi(min(row0 + S::BM, P.nrows) - 1);
+    const int lo = max(P.kv_lo(row0), 0) / BN * BN;
+    if (lo < hi && !grp_b) issue_rows(hi, lo, k0, BoolC<false>{});
+  };
+  start_tile();
+
+  for (;;) {
+
+  const int nrows = P.nrows;
+  const int row_last = min(row0 + S::BM, nrows) - 1;
+  const int wg_lo = P.kv_lo(row0);
+  const int wg_hi = P.kv_hi(row_last);
+
+  const int wrow0 = row0 + wave * 32;
+  const bool wave_active = wrow0 < nrows;
+  const int wrow_last = min(wrow0 + 31, nrows - 1);
+  const int w_lo_min = wave_active ? P.kv_lo(wrow0) : 0;
+  const int w_lo_max = wave_active ? P.kv_lo(wrow_last) : 0;
+  const int w_hi_min = wave_active ? P.kv_hi(wrow0) : 0;
+  const int w_hi_max = wave_active ? P.kv_hi(wrow_last) : 0;
+
+  const int row = wrow0 + lr;
+  const bool row_valid = row < nrows;
+  const int my_lo = row_valid ? P.kv_lo(row) : 0;
+  const int my_hi = row_valid ? P.kv_hi(row) : 0;
 
   f32x16 o[D / 32];
 #pragma unroll
@@ -414,51 +475,10 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   // were in period j-1, before its barrier.  The loop body covers two tiles
   // so that every buffer is a compile-time array (see the note on k0..v1
   // above).
-  const bool grp_b = wave >= S::NW / 2;
   const int j0 = max(wg_lo, 0) / BN;
   const int j1 = (wg_hi + BN - 1) / BN;
-  // K / V rows are a base plus a row stride: tiles are DMA'd through buffer
-  // resources, the lane's byte offset within the tile is fixed, the tile
-  // base is scalar, and rows at or past the last key read as zero (their
-  // scores are masked).  Group A alone issues them, from inside its matrix
-  // phase: issuing 32 KB per tile from all eight waves at the start of a
-  // slot stalled them on the vector-memory queue; behind a burst of MFMAs
-  // the queueing overlaps the matrix core's work (wave w < 4 fills 1 KB
-  // blocks 4w .. 4w+3, i.e. keys n0 + 16w .. n0 + 16w + 15).  A wave's 16
-  // rows are a base plus the row stride: for paged K / V (pages of at least
-  // 16 keys) they lie in one page, whose block-table entry is one scalar
-  // load per wave and tile.
-  constexpr int DB = 16 / (S::NW / 2);  // blocks per DMA wave
-  static_assert(DB * 4 == 16, "each DMA wave fills 16 rows");
-  uint32_t k_loff[DB], v_loff[DB];
-#pragma unroll
-  for (int ii = 0; ii < DB; ++ii) {
-    const int r = 4 * (DB * wave + ii) + (lane >> 4);  // row of the tile
-    const uint32_t r16 = 4 * ii + (lane >> 4);         // row of the wave's 16
-    const uint32_t chunk = 8u * ((lane & 15) ^ swz_chunk(r));
-    k_loff[ii] = 2u * (r16 * (uint32_t)P.k_row_stride() + chunk);
-    v_loff[ii] = 2u * (r16 * (uint32_t)P.v_row_stride() + chunk);
-  }
-  auto issue_rows = [&](int n0, char* dst, auto is_v) {
-    constexpr bool kV = decltype(is_v)::value;
-    const int nw = n0 + 16 * wave;
-    const int nvalid = min(16, wg_hi - nw);  // n0 < wg_hi, so n0's row resolves
-    const int nb = nvalid > 0 ? nw : n0;
-    const uint16_t* base = kV ? P.v_ptr(nb) : P.k_ptr(nb);
-    // The range ends after the last valid row's D columns (not nvalid whole
-    // strides): a size-1 sequence dimension may come with stride 0.
-    const uint32_t bytes = span_bytes(nvalid, kV ? P.v_row_stride() : P.k_row_stride(), D);
-    u32x4 rs = rsrc_words(base, bytes);
-    // Uniform by construction (the block-table read of a paged problem is
-    // not known to be); the resource must sit in scalar registers.
-#pragma unroll
-    for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(rs[w]);
-#pragma unroll
-    for (int ii = 0; ii < DB; ++ii)
-      buffer_lds16_opaque(rs, kV ? v_loff[ii] : k_loff[ii], dst + (DB * wave + ii) * 1024);
-  };
-  auto issue_k = [&](int n0, char* kb) { issue_rows(n0, kb, BoolC<false>{}); };
-  auto issue_v = [&](int n0, char* vb) { issue_rows(n0, vb, BoolC<true>{}); };
+  auto issue_k = [&](int n0, char* kb) { issue_rows(wg_hi, n0, kb, BoolC<false>{}); };
+  auto issue_v = [&](int n0, char* vb) { issue_rows(wg_hi, n0, vb, BoolC<true>{}); };
   // One slot: the matrix phase for tile j (O of j-1 from vprev, S of j from
   // kcur; group A also issues the DMA of K(j+1) into knext and V(j) into
   // vcur) or the softmax phase for tile js.
@@ -482,7 +502,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (j0 < j1 && !grp_b) issue_k(j0 * BN, k0);
+  // The tile's Q rows and first K tile (start_tile) have landed.
   wait_vmem();
   __syncthreads();
   // Each group runs its own copy of the loop (the barriers pair up across
@@ -509,9 +529,20 @@ __device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, floa
   else
     run(BoolC<false>{});
 
+  // Every wave is past the loop's last barrier: LDS and qf are free.
   const float l_all = l_run + swap_halves(l_run);
-  if (!row_valid) return;
-  fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
+  if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
+  if (!next(P, row0)) break;
+  start_tile();
+  }
+}
+
+// One row tile.
+template <class T, class Prob>
+__device__ __forceinline__ void attn_fwd_tile_d128(const Prob& P, int row0, float scale,
+                                                   char* k0, char* v0, char* k1, char* v1) {
+  attn_fwd_tiles_d128<T>(P, row0, scale, k0, v0, k1, v1, [](Prob&, int&) { return false; });
 }
 
 }  // namespace fa
+

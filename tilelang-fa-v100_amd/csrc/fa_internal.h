@@ -4,6 +4,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <stdint.h>
+
+#include <algorithm>
 
 #include "fa355.h"
 #include "fa_tiles.h"
@@ -27,6 +30,17 @@ hipError_t launch_paged_prefill_split(const fa_paged_args& a, int nsplit, void* 
 
 // Compute units of the current device (cached per device).
 int device_cu_count();
+
+// Grid of a persistent launch over ntiles x nbh tiles (persistent_tile in
+// fa_common.h): per_cu workgroups per CU, fewer when there are fewer tiles,
+// a multiple of 8 when nbh is one (each workgroup then stays on one XCD's
+// heads).
+inline int persistent_grid(int ntiles, int nbh, int per_cu) {
+  const int64_t total = (int64_t)ntiles * nbh;
+  int64_t w = std::min<int64_t>(total, (int64_t)per_cu * device_cu_count());
+  if (nbh % 8 == 0) w = std::max<int64_t>(8, w / 8 * 8);
+  return (int)w;
+}
 
 int decode_num_splits(const fa_decode_args& a);
 size_t decode_workspace_bytes(const fa_decode_args& a);
