@@ -159,20 +159,28 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
   }
 
   // Tile t covers query head hk*G + t / nit and query tile it1 - 1 - t % nit
-  // (query tiles are swept from the last down within each head); (h_rel, it)
-  // is carried incrementally so the loop has no integer division.
-  auto issue_q = [&](int h_rel, int it, int qo, int oo, int so) {
-    const int h = hk * G + h_rel;
+  // (query tiles are swept from the last down within each head).  The tile
+  // to issue next is carried as (h_rel, it) and as running addresses of its
+  // first Q / dO row and statistics, stepped back by one tile per iteration
+  // and rebuilt when the head changes: no integer division and no 64-bit
+  // products per tile (those were ~100 scalar instructions per tile).
+  const int64_t qs1 = a.q_stride[1], os1 = a.do_stride[1];
+  const uint16_t* q_top = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] +
+                          (int64_t)(hk * G) * a.q_stride[2] + (int64_t)(max(it1, 1) - 1) * S::BQ * qs1;
+  const uint16_t* o_top = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
+                          (int64_t)(hk * G) * a.do_stride[2] +
+                          (int64_t)(max(it1, 1) - 1) * S::BQ * os1;
+  const float* s_top = stats + 2 * head_rows * Sq + (max(it1, 1) - 1) * S::BQ;
+  const uint16_t* q_i = q_top;
+  const uint16_t* o_i = o_top;
+  const float* s_i = s_top;
+  auto issue_q = [&](int it, int qo, int oo, int so) {
     const int i0 = it * S::BQ;
     // Buffer resources over the tile's valid rows: rows at or past Sq read
     // as zero (their products are masked), so no row clamping is needed.
-    const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + b * a.q_stride[0] +
-                           h * a.q_stride[2] + (int64_t)i0 * a.q_stride[1];
-    const uint16_t* orow = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
-                           h * a.do_stride[2] + (int64_t)i0 * a.do_stride[1];
     const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
-    const u32x4 rq = rsrc_words(qrow, span_bytes(nrows, a.q_stride[1], D));
-    const u32x4 ro = rsrc_words(orow, span_bytes(nrows, a.do_stride[1], D));
+    const u32x4 rq = rsrc_words(q_i, span_bytes(nrows, qs1, D));
+    const u32x4 ro = rsrc_words(o_i, span_bytes(nrows, os1, D));
     // Opaque DMA: the loop's wait_vmem + barrier is the only wait the tile
     // needs.
 #pragma unroll
@@ -183,9 +191,22 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
     }
     if (wave == 0) {
       // Lanes 0-31 fetch LSE*log2(e), lanes 32-63 rowdot ([B*H][2][Sq]).
-      const float* sbase = stats + 2 * (head_rows + h_rel) * Sq + i0;
       const unsigned lo = (lane >> 5) * Sq + min(lane & 31, Sq - 1 - i0);
-      global_lds4_opaque(sbase + lo, smem + so);
+      global_lds4_opaque(s_i + lo, smem + so);
+    }
+  };
+  // The next tile to issue, and its addresses.
+  auto advance_issue = [&](int& h_rel, int& it) {
+    if (it-- == it0) {
+      it = it1 - 1;
+      ++h_rel;
+      q_i = q_top + h_rel * a.q_stride[2];
+      o_i = o_top + h_rel * a.do_stride[2];
+      s_i = s_top + 2 * h_rel * Sq;
+    } else {
+      q_i -= S::BQ * qs1;
+      o_i -= S::BQ * os1;
+      s_i -= S::BQ;
     }
   };
 
@@ -300,15 +321,15 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
   // then the DMA of tile t+1 and tile t's products.  The loop covers two
   // tiles so that every buffer offset is an instruction immediate.
   if (ntot > 0) {
-    issue_q(ih, ii, OFF_Q0, OFF_O0, OFF_ST0);
-    advance(ih, ii);
+    issue_q(ii, OFF_Q0, OFF_O0, OFF_ST0);
+    advance_issue(ih, ii);
   }
   for (int t = 0; t < ntot; t += 2) {
     wait_vmem();
     __syncthreads();
     if (t + 1 < ntot) {
-      issue_q(ih, ii, OFF_Q1, OFF_O1, OFF_ST1);
-      advance(ih, ii);
+      issue_q(ii, OFF_Q1, OFF_O1, OFF_ST1);
+      advance_issue(ih, ii);
     }
     step(ci, OFF_Q0, OFF_O0, OFF_ST0);
     advance(ch, ci);
@@ -316,8 +337,8 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
     wait_vmem();
     __syncthreads();
     if (t + 2 < ntot) {
-      issue_q(ih, ii, OFF_Q0, OFF_O0, OFF_ST0);
-      advance(ih, ii);
+      issue_q(ii, OFF_Q0, OFF_O0, OFF_ST0);
+      advance_issue(ih, ii);
     }
     step(ci, OFF_Q1, OFF_O1, OFF_ST1);
     advance(ch, ci);
