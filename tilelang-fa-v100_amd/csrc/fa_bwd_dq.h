@@ -151,21 +151,36 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
   // ---- tile loader: wave w fills 1 KB blocks BPW w .. BPW w + BPW - 1 of
-  // the K and V tiles; lane l of block blk holds row RPB blk + l / CPR,
-  // stored chunk l % CPR (logical chunk (l % CPR) ^ swz(row)).  Rows past
-  // the last key repeat it (their scores are masked).
+  // the K and V tiles, i.e. the tile's rows WR w .. WR w + WR - 1; lane l of
+  // block blk holds row RPB blk + l / CPR, stored chunk l % CPR (logical
+  // chunk (l % CPR) ^ swz(row)).  The rows go through buffer resources based
+  // at the wave's first row: the lane's byte offset is fixed for the whole
+  // loop (below 8 rows, so 32 bits hold it for any sequence stride below
+  // 2^26), and rows at or past the last key read as zero (their scores are
+  // masked).
+  constexpr int WR = S::RPB * S::BPW;
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
-  const int ld_last = max(wg_hi - 1, 0);
+  uint32_t k_loff[S::BPW], v_loff[S::BPW];
+#pragma unroll
+  for (int ii = 0; ii < S::BPW; ++ii) {
+    const int rr = S::RPB * ii + lane / S::CPR;  // row within the wave's WR rows
+    const int c = (lane % S::CPR) ^ swz(WR * wave + rr);
+    k_loff[ii] = 2u * (rr * (uint32_t)a.k_stride[1] + 8 * c);
+    v_loff[ii] = 2u * (rr * (uint32_t)a.v_stride[1] + 8 * c);
+  }
   auto issue_tile = [&](int n0, char* kb, char* vb) {
+    const int nb = n0 + WR * wave;
+    const uint32_t nvalid = (uint32_t)max(min(WR, wg_hi - nb), 0);
+    const u32x4 rk = rsrc_words(kg + (int64_t)nb * a.k_stride[1],
+                                span_bytes(nvalid, a.k_stride[1], D));
+    const u32x4 rv = rsrc_words(vg + (int64_t)nb * a.v_stride[1],
+                                span_bytes(nvalid, a.v_stride[1], D));
 #pragma unroll
     for (int ii = 0; ii < S::BPW; ++ii) {
       const int blk = S::BPW * wave + ii;
-      const int r = S::RPB * blk + lane / S::CPR;
-      const int c = (lane % S::CPR) ^ swz(r);
-      const int n = min(n0 + r, ld_last);
-      global_lds16_opaque(kg + (int64_t)n * a.k_stride[1] + 8 * c, kb + blk * 1024);
-      global_lds16_opaque(vg + (int64_t)n * a.v_stride[1] + 8 * c, vb + blk * 1024);
+      buffer_lds16_opaque(rk, k_loff[ii], kb + blk * 1024);
+      buffer_lds16_opaque(rv, v_loff[ii], vb + blk * 1024);
     }
   };
 
