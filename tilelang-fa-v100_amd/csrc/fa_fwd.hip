@@ -213,8 +213,14 @@ struct PagedRows {
     return lse + (r - t * G) * lse_head + t;
   }
   __device__ int64_t page_of(int n) const {
-    // Clamp guards against a corrupt table; valid tables are unaffected.
-    return (int64_t)min((unsigned)bt[n >> ps_log2], (unsigned)last_page);
+    // The block table is read-only for the kernel's lifetime: through a
+    // constant-address-space pointer a wave-uniform n reads it with a scalar
+    // load (waited for on lgkmcnt).  A plain load compiled to a vector load
+    // followed by vmcnt(0), which also waited for every K / V tile DMA in
+    // flight, twice per tile.  The clamp guards against a corrupt table;
+    // valid tables are unaffected.
+    const auto* btc = (const __attribute__((address_space(4))) int32_t*)bt;
+    return (int64_t)min((unsigned)btc[n >> ps_log2], (unsigned)last_page);
   }
   __device__ const uint16_t* k_ptr(int n) const {
     return kc + page_of(n) * k_page + (n & ps_mask) * k_slot;
