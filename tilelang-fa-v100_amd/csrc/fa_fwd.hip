@@ -161,11 +161,19 @@ void fwd_dense_kernel(fa_fwd_args a) {
     P.has_lse = ap->lse != nullptr;
     row0 = qt * C::BM;
   };
+  DenseRows P;
+  int row0 = 0;
+  if constexpr (MODE == kMaskBand) {
+    // A band from the arguments costs the core registers (the tile loop
+    // around it spilled inside the key loop): one workgroup per tile.
+    if (blockIdx.x >= (unsigned)(qtiles * nbh)) return;
+    setup(blockIdx.x, P, row0);
+    run_fwd_tile<T, D, true>(P, row0, a.softmax_scale);
+    return;
+  }
   int r = 0;
   const int vid = persistent_tile(blockIdx.x, gridDim.x, r, qtiles * nbh, nbh);
   if (vid < 0) return;
-  DenseRows P;
-  int row0 = 0;
   setup(vid, P, row0);
   run_fwd_tiles<T, D, true>(P, row0, a.softmax_scale, [&](DenseRows& Pn, int& rn) {
     const int v = persistent_tile(blockIdx.x, gridDim.x, ++r, qtiles * nbh, nbh);
@@ -458,8 +466,12 @@ template <class T, int D>
 static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   using C = FwdKernelCfg<D, true>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
-  const dim3 grid((unsigned)persistent_grid(qtiles, a.num_heads * a.batch, C::WG_PER_CU));
   const int mode = mask_mode(a);
+  // Band instances run one workgroup per tile (fwd_dense_kernel).
+  const bool band = mode == kMaskBand || (D == 256 && T::kId == FA_DTYPE_BF16);
+  const dim3 grid((unsigned)(band ? qtiles * a.num_heads * a.batch
+                                  : persistent_grid(qtiles, a.num_heads * a.batch,
+                                                    C::WG_PER_CU)));
   if constexpr (D == 256 && T::kId == FA_DTYPE_BF16) {
     // bf16 at head_dim 256: the band instance (band from the arguments; causal
     // and full attention are bands too) for every mode.  The causal and
