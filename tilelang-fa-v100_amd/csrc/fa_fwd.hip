@@ -267,21 +267,47 @@ struct PagedSplitRows : PagedRows {
 
 // Finds the sequence owning `tile` in the varlen tile space where sequence b
 // has ceil(qlen_b * G / BM) tiles.  Returns b (or -1) and the tile index
-// within the sequence.  Wave 0 scans query_start_loc 64 sequences at a time
-// with a shuffle prefix sum and finds the owner with a ballot; one barrier
-// hands the result to the other waves (a block-wide scan in LDS took 16
-// barriers).
-__device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
-                             int tile, int* local) {
+// within the sequence.  Wave 0 scans the sequences 64 at a time with a
+// shuffle prefix sum and finds the owner with a ballot; one barrier hands
+// the result to the other waves (a block-wide scan in LDS took 16
+// barriers).  Up to 64 sequences are taken in order of decreasing history
+// (prefix_kv_lens; equal histories keep their order): a sequence's tiles all
+// see about its history plus its own length in keys, so with the
+// heaviest-first order inside each sequence the tiles go out roughly
+// longest first, and the last workgroups on each CU are short (C5, chunked
+// prefill with histories of 0-8k keys: 2% faster; 5% less idle time in a
+// dispatch simulation, part of it spent on the sort).  When all histories
+// are equal the order is the sequences' own.
+__device__ int find_sequence(const int32_t* qsl, const int32_t* prefix, int batch, int G,
+                             int BM, int tile, int* local) {
   __shared__ int found_b, found_local;
   if (wave_id() == 0) {
     const int lane = threadIdx.x & 63;
     int base = 0, fb = -1, fl = 0;
-    for (int c0 = 0; c0 < batch; c0 += 64) {
-      const int b = c0 + lane;
+    // The sort costs wave 0 about a microsecond of dependent shuffles; it is
+    // skipped when the histories are all equal (the order would not change).
+    const bool sort = batch <= 64 &&
+                      __ballot(lane < batch && prefix[lane] != prefix[0]) != 0;
+    if (sort) {
+      // Bitonic sort of (history descending, index ascending) across lanes;
+      // lanes past the batch sort last.
+      const uint32_t hist = lane < batch ? (uint32_t)max(prefix[lane], 0) : 0u;
+      uint64_t key = lane < batch ? ((uint64_t)(0x7fffffffu - hist) << 32) | (uint32_t)lane
+                                  : ~0ull;
+#pragma unroll
+      for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), j) << 32) |
+                                 (uint32_t)__shfl_xor((int)(uint32_t)key, j);
+          const bool up = (lane & k) == 0, lower = (lane & j) == 0;
+          const uint64_t lo = key < other ? key : other, hi = key < other ? other : key;
+          key = (up == lower) ? lo : hi;
+        }
+      const int sb = key == ~0ull ? batch : (int)(uint32_t)key;  // sequence at this lane
       int n = 0;
-      if (b < batch) {
-        const int ql = qsl[b + 1] - qsl[b];
+      if (sb < batch) {
+        const int ql = qsl[sb + 1] - qsl[sb];
         n = ql > 0 ? (int)(((int64_t)ql * G + BM - 1) / BM) : 0;
       }
       int incl = n;
@@ -291,15 +317,38 @@ __device__ int find_sequence(const int32_t* qsl, int batch, int G, int BM,
         if (lane >= off) incl += v;
       }
       const int excl = incl - n;
-      const bool hit = b < batch && n > 0 && tile >= base + excl && tile < base + incl;
+      const bool hit = sb < batch && n > 0 && tile >= excl && tile < incl;
       const uint64_t m = __ballot(hit);
       if (m) {
         const int src = __ffsll((unsigned long long)m) - 1;
-        fb = c0 + src;
-        fl = tile - base - __shfl(excl, src);
-        break;
+        fb = __shfl(sb, src);
+        fl = tile - __shfl(excl, src);
       }
-      base += __shfl(incl, 63);
+    } else {
+      for (int c0 = 0; c0 < batch; c0 += 64) {
+        const int b = c0 + lane;
+        int n = 0;
+        if (b < batch) {
+          const int ql = qsl[b + 1] - qsl[b];
+          n = ql > 0 ? (int)(((int64_t)ql * G + BM - 1) / BM) : 0;
+        }
+        int incl = n;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int v = __shfl_up(incl, off);
+          if (lane >= off) incl += v;
+        }
+        const int excl = incl - n;
+        const bool hit = b < batch && n > 0 && tile >= base + excl && tile < base + incl;
+        const uint64_t m = __ballot(hit);
+        if (m) {
+          const int src = __ffsll((unsigned long long)m) - 1;
+          fb = c0 + src;
+          fl = tile - base - __shfl(excl, src);
+          break;
+        }
+        base += __shfl(incl, 63);
+      }
     }
     if (lane == 0) {
       found_b = fb;
@@ -358,7 +407,7 @@ void fwd_paged_kernel(fa_paged_args a) {
   const int slot = id % slots;
 
   int local = 0;
-  const int b = find_sequence(a.query_start_loc, a.batch, G, S::BM, slot, &local);
+  const int b = find_sequence(a.query_start_loc, a.prefix_kv_lens, a.batch, G, S::BM, slot, &local);
   if (b < 0) return;
   const int qs = a.query_start_loc[b];
   const int qlen = a.query_start_loc[b + 1] - qs;
@@ -387,7 +436,7 @@ void fwd_paged_split_kernel(fa_paged_args a, int nsplit, float* po, float* plse)
   const int slot = id % slots;
 
   int local = 0;
-  const int b = find_sequence(a.query_start_loc, a.batch, G, S::BM, slot, &local);
+  const int b = find_sequence(a.query_start_loc, a.prefix_kv_lens, a.batch, G, S::BM, slot, &local);
   if (b < 0) return;
   const int qs = a.query_start_loc[b];
   const int qlen = a.query_start_loc[b + 1] - qs;
