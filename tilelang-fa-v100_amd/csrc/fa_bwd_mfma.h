@@ -42,6 +42,11 @@ struct BwdShapeMfma {
   static_assert(QT_BLOCKS % NW == 0 && (K_BYTES / 1024) % NW == 0, "DMA split");
 };
 
+// A operands (dOᵀ, Qᵀ) of one dVᵀ / dKᵀ product pair.
+struct TrOps {
+  u32x4 ao, aq;
+};
+
 // MODE (MaskMode): full attention, causal, or a window band from the arguments.
 template <class T, int D_, int MODE>
 __global__ __launch_bounds__((64 * BwdShapeMfma<D_>::NW), (BwdShapeMfma<D_>::WPE))
@@ -135,6 +140,15 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
+  // D = 256: dK / dV (32 keys x 256 d) fill the 256 AGPRs and stay there
+  // (mma32_agpr); everything else fits the 256 VGPRs.
+  if constexpr (D == 256) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      agpr_fence_in(dk[dt]);
+      agpr_fence_in(dv[dt]);
+    }
+  }
 
   const int q_begin = CAUSAL ? band.first_row(kv0) : 0;
   const int q_end = CAUSAL ? band.end_row(kv0 + S::BKV - 1, Sq) : Sq;
@@ -292,21 +306,33 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
         sB[kq][w] = T::pack(dp[e], dp[e + 1]);
       }
     // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads)
+    auto tr_ops = [&](int kq, int dt) {
+      const int ro = kq * 16 * S::ROWB;
+      const u32x2 o_lo = lds_read_tr(ob + toff(0, dt) + ro);
+      const u32x2 o_hi = lds_read_tr(ob + toff(1, dt) + ro);
+      const u32x2 q_lo = lds_read_tr(qb + toff(0, dt) + ro);
+      const u32x2 q_hi = lds_read_tr(qb + toff(1, dt) + ro);
+      return TrOps{{o_lo[0], o_lo[1], o_hi[0], o_hi[1]}, {q_lo[0], q_lo[1], q_hi[0], q_hi[1]}};
+    };
+    if constexpr (D == 256) {
+      lds_pipeline<2 * (D / 32), 2>(
+          [&](int k) { return tr_ops(k / (D / 32), k % (D / 32)); },
+          [&](int k, const TrOps& o) {
+            const int kq = k / (D / 32), dt = k % (D / 32);
+            mma32_agpr<T>(dv[dt], o.ao, pB[kq]);
+            mma32_agpr<T>(dk[dt], o.aq, sB[kq]);
+          });
+    } else {
 #pragma unroll
-    for (int kq = 0; kq < 2; ++kq)
+      for (int kq = 0; kq < 2; ++kq)
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const int ro = kq * 16 * S::ROWB;
-        const u32x2 o_lo = lds_read_tr(ob + toff(0, dt) + ro);
-        const u32x2 o_hi = lds_read_tr(ob + toff(1, dt) + ro);
-        const u32x2 q_lo = lds_read_tr(qb + toff(0, dt) + ro);
-        const u32x2 q_hi = lds_read_tr(qb + toff(1, dt) + ro);
-        const u32x4 ao = {o_lo[0], o_lo[1], o_hi[0], o_hi[1]};
-        const u32x4 aq = {q_lo[0], q_lo[1], q_hi[0], q_hi[1]};
-        dv[dt] = T::mma32(ao, pB[kq], dv[dt]);
-        dk[dt] = T::mma32(aq, sB[kq], dk[dt]);
-      }
-    sched_pipeline<2 * (D / 32), 4, 2, 2>();
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const TrOps o = tr_ops(kq, dt);
+          dv[dt] = T::mma32(o.ao, pB[kq], dv[dt]);
+          dk[dt] = T::mma32(o.aq, sB[kq], dk[dt]);
+        }
+      sched_pipeline<2 * (D / 32), 4, 2, 2>();
+    }
   };
 
   auto advance = [&](int& h_rel, int& it) {
@@ -344,6 +370,13 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
     advance(ch, ci);
   }
   wait_vmem();
+  if constexpr (D == 256) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      agpr_fence_out(dk[dt]);
+      agpr_fence_out(dv[dt]);
+    }
+  }
 
   const float sc = a.softmax_scale;
   const int my_kv = kvw + lr;

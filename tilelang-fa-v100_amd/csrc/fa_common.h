@@ -114,6 +114,34 @@ struct BFloat16 {
   }
 };
 
+// acc += A·B on v_mfma_f32_32x32x16 with `acc` held in the accumulation
+// registers (AGPRs) for its whole life.  For kernels whose accumulators fill
+// the AGPR file next to a full VGPR file, the register allocator otherwise
+// shuffles 16-register tuples between the two files and within the AGPRs
+// (v_accvgpr_mov / read / write around every product).  The compiler's hazard
+// pass does not look inside inline assembly, so the statement carries its
+// own wait states: `s_nop 2` covers a VALU write of A or B just before it (2
+// wait states are required); chained products on the same accumulator need
+// none.  Callers publish zero-initialised accumulators to the asm with
+// agpr_fence_in() and read results only after agpr_fence_out().
+template <class T>
+__device__ __forceinline__ void mma32_agpr(f32x16& acc, u32x4 a, u32x4 b) {
+  if constexpr (T::kId == 0)
+    asm("s_nop 2\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// After the VALU writes that initialise `acc` (2 wait states before an MFMA
+// reads them as C).
+__device__ __forceinline__ void agpr_fence_in(f32x16& acc) {
+  asm volatile("s_nop 2" : "+a"(acc));
+}
+// Before any VALU read of `acc`: an 8- or 16-pass XDL write needs 11 or 19
+// wait states before a VALU instruction reads the result.
+__device__ __forceinline__ void agpr_fence_out(f32x16& acc) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(acc));
+}
+
 // Low 16 bits of `a` and of `b` packed as {a.lo, b.lo}; likewise for the high
 // halves.  Used to transpose 16-bit matrices held in registers.
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
