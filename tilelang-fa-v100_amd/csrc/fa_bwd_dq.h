@@ -149,6 +149,12 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+  // D = 256: the dQ accumulators (32 rows x 256 d, 128 registers) stay in
+  // AGPRs (mma32_agpr) and Q / dO rows, scores and operands in VGPRs.
+  if constexpr (D == 256) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) agpr_fence_in(acc[dt]);
+  }
 
   // ---- tile loader: wave w fills 1 KB blocks BPW w .. BPW w + BPW - 1 of
   // the K and V tiles, i.e. the tile's rows WR w .. WR w + WR - 1; lane l of
@@ -252,7 +258,10 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
           [&](int k, const KtOps& r) {
             const int dt = k % (D / 32);
             const u32x4 ak = {r.lo[0], r.lo[1], r.hi[0], r.hi[1]};
-            acc[dt] = T::mma32(ak, sb[k / (D / 32)], acc[dt]);
+            if constexpr (D == 256)
+              mma32_agpr<T>(acc[dt], ak, sb[k / (D / 32)]);
+            else
+              acc[dt] = T::mma32(ak, sb[k / (D / 32)], acc[dt]);
           });
     }
   };
@@ -275,6 +284,10 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
   }
 
   // ---- dQ = scale · Σ dS K; acc[dt][4g + r] = dQ[row][32dt + 8g + 4lh + r].
+  if constexpr (D == 256) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) agpr_fence_out(acc[dt]);
+  }
   if (!row_valid) return;
   const float sc = a.softmax_scale;
   uint16_t* dqp = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] +
