@@ -47,9 +47,9 @@ struct DenseRows {
   __device__ int64_t v_row_stride() const { return vs; }
 };
 
-// Tile geometry per head_dim and core: D = 128 (both schedules) and D = 256
-// with PP (two-phase schedule) use the direct-to-LDS 8-wave cores, the rest
-// the 4-wave core.
+// Tile geometry per head_dim and core: D = 128 (both schedules) uses the
+// direct-to-LDS 8-wave cores, D = 256 with PP the direct-to-LDS one-pass
+// 4-wave core, the rest the register-staged 4-wave core.
 template <int D, bool PP>
 struct FwdKernelCfg {
   static constexpr int BM = FwdShape<D>::BM;
@@ -61,10 +61,10 @@ struct FwdKernelCfg {
 template <>
 struct FwdKernelCfg<256, true> {
   static constexpr int BM = FwdShapeD256::BM;
-  static constexpr int THREADS = 512;
-  static constexpr int WAVES_PER_EU = 2;
+  static constexpr int THREADS = 64 * FwdShapeD256::NW;
+  static constexpr int WAVES_PER_EU = 1;
   static constexpr int WG_PER_CU = 1;
-  static constexpr int LDS_BYTES = FwdShapeD256::LDS_BYTES;
+  static constexpr int LDS_BYTES = 4 * FwdShapeD256::TILEB;
 };
 template <bool PP>
 struct FwdKernelCfg<128, PP> {
@@ -90,9 +90,8 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
     else
       attn_fwd_tile_d128_plain<T>(P, row0, scale, k0, v0, k1, v1);
   } else if constexpr (D == 256 && PP) {
-    using S = FwdShapeD256;
-    __shared__ __attribute__((aligned(16))) char k0[S::KTILEB], v0[S::VTILEB], k1[S::KTILEB],
-        v1[S::VTILEB];
+    constexpr int B = FwdShapeD256::TILEB;
+    __shared__ __attribute__((aligned(16))) char k0[B], v0[B], k1[B], v1[B];
     attn_fwd_tile_d256<T>(P, row0, scale, k0, v0, k1, v1);
   } else {
     __shared__ __attribute__((aligned(16))) uint16_t smem[FwdShape<D>::LDS_ELEMS];
@@ -517,27 +516,16 @@ static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const int mode = mask_mode(a);
   // Band instances run one workgroup per tile (fwd_dense_kernel).
-  const bool band = mode == kMaskBand || (D == 256 && T::kId == FA_DTYPE_BF16);
+  const bool band = mode == kMaskBand;
   const dim3 grid((unsigned)(band ? qtiles * a.num_heads * a.batch
                                   : persistent_grid(qtiles, a.num_heads * a.batch,
                                                     C::WG_PER_CU)));
-  if constexpr (D == 256 && T::kId == FA_DTYPE_BF16) {
-    // bf16 at head_dim 256: the band instance (band from the arguments; causal
-    // and full attention are bands too) for every mode.  The causal and
-    // full instances spilled 190 VGPRs in the loop (the fp32 row sum of
-    // bf16 keeps more values live than fp16's packed-word sum, and the
-    // register allocator lost the two-waves-per-SIMD budget); the band
-    // instance fits 230 without spills.
-    (void)mode;
+  if (mode == kMaskCausal)
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskCausal>), grid, dim3(C::THREADS), 0, st, a);
+  else if (band)
     hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskBand>), grid, dim3(C::THREADS), 0, st, a);
-  } else {
-    if (mode == kMaskCausal)
-      hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskCausal>), grid, dim3(C::THREADS), 0, st, a);
-    else if (mode == kMaskBand)
-      hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskBand>), grid, dim3(C::THREADS), 0, st, a);
-    else
-      hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskNone>), grid, dim3(C::THREADS), 0, st, a);
-  }
+  else
+    hipLaunchKernelGGL((fwd_dense_kernel<T, D, kMaskNone>), grid, dim3(C::THREADS), 0, st, a);
   return hipGetLastError();
 }
 
@@ -556,9 +544,9 @@ hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st) {
                                   : dispatch_dense_d<Half>(a, st);
 }
 
-// The two-phase D = 128 / 256 cores take K / V in runs of 16 (D = 128) or
-// 8 (D = 256) keys at a fixed row stride: pages of at least 16 keys, token
-// strides below 2^24 elements.
+// The D = 128 ping-pong core and the D = 256 core take K / V in runs of 16
+// (D = 128) or 8 (D = 256) keys at a fixed row stride: pages of at least 16
+// keys, token strides below 2^24 elements.
 static bool paged_pingpong(const fa_paged_args& a) {
   const int64_t lim = int64_t(1) << 24;
   return (a.head_dim == 128 || a.head_dim == 256) && a.page_size >= 16 &&

@@ -1,24 +1,21 @@
-// Attention forward core for head_dim 256 on gfx950: the two-phase
-// (ping-pong) schedule of attn_fwd_tile_d128 with the operands resized.
-//
-//  * 8 waves x 32 query rows (256 rows per workgroup), two waves per SIMD:
-//    Q stays in registers (64), and O is accumulated in two passes of 128
-//    columns (64 registers), the scores being recomputed in the second
-//    pass.  One pass holding all 256 columns needs ~400 registers, i.e. one
-//    wave per SIMD and no partner to overlap the matrix and softmax phases.
-//    Both passes run the same online softmax over the same scores, so their
-//    running max and sum agree and each pass normalises its own columns.
-//  * 32-key tiles.  A K tile is 32 rows of 512 bytes (16 KB); a pass's V
-//    tile holds only that pass's 128 columns (32 rows of 256 bytes, 8 KB).
-//  * K rows: 16-byte chunk q of row r is stored at chunk q ^ swz(r) (the
-//    XOR touches the low four chunk bits, so chunks stay in their 256-byte
-//    half).  The Sᵀ = K Qᵀ operand of step c (logical chunk 2c + lh of row
-//    lr) then sits at base ^ 32c with one base per lane.  V rows use the
-//    256-byte layout of the head_dim 128 core, so its Vᵀ transpose reads
-//    carry over.
-//  * DMA as in the head_dim 128 core: group A's four waves each fill 8
-//    consecutive keys of K and of V through a buffer resource, from inside
-//    their matrix phase.
+// Attention forward core for head_dim 256 on gfx950 (dense rows, and paged
+// rows with pages of at least 16 keys): 4 waves x 32 query rows (128 rows
+// per workgroup), one wave per SIMD, 32-key tiles.
+//  * O (32 rows x 256 d, 128 registers) lives in AGPRs for the whole tile
+//    (mma32_agpr), Q (64) and the scores in VGPRs: one pass over the keys
+//    with 512 registers per wave.  (Two waves per SIMD would need O in two
+//    128-column passes with the scores recomputed, 1.5x the products.)
+//  * Software pipeline inside the wave: the scores of tile j + 1 are
+//    computed while tile j is exponentiated (the max, rescale decision and
+//    exponentials are spread between the 16 products of Sᵀ(j + 1)), then
+//    Oᵀ += Vᵀ(j) Pᵀ(j).  The wave's matrix core has no partner wave to
+//    overlap with, so the overlap has to come from its own instruction
+//    stream.
+//  * K and V tiles are 32 rows of 512 bytes; 16-byte chunk q of row r is
+//    stored at chunk q ^ swz(r), the XOR touching the low four chunk bits
+//    (chunks stay in their 256-byte half).  Double buffered: iteration j
+//    reads K(j + 1) and V(j) while K(j + 2) and V(j + 1) stream in.  Each
+//    wave DMAs 8 rows of each (four 1 KB blocks) through a buffer resource.
 #pragma once
 
 #include "fa_common.h"
@@ -28,30 +25,23 @@ namespace fa {
 
 struct FwdShapeD256 {
   static constexpr int D = 256;
-  static constexpr int DO = 128;              // O columns per pass
-  static constexpr int NPASS = D / DO;
-  static constexpr int BM = tiles::kFwd256Rows;   // query rows per workgroup
-  static constexpr int BN = tiles::kFwd256Keys;   // keys per tile
-  static constexpr int NW = tiles::kFwd256Waves;  // waves
-  static constexpr int KROWB = 2 * D;          // bytes per K row
-  static constexpr int VROWB = 2 * DO;         // bytes per V row of one pass
-  static constexpr int KTILEB = BN * KROWB;    // 16 KB
-  static constexpr int VTILEB = BN * VROWB;    // 8 KB
-  static constexpr int LDS_BYTES = 2 * (KTILEB + VTILEB);
-  static_assert(BN == 32 && NW == 8, "one 32-key block per tile, two wave groups of four");
+  static constexpr int BM = tiles::kFwd256Rows;  // 4 waves x 32 rows
+  static constexpr int BN = 32;
+  static constexpr int NW = 4;
+  static constexpr int ROWB = 2 * D;         // bytes per K / V row
+  static constexpr int TILEB = BN * ROWB;    // 16 KB
+  static_assert(BM == 32 * NW, "one 32-row block per wave");
 };
 
-// k0/v0 and k1/v1 are four distinct __shared__ arrays (KTILEB and VTILEB
-// bytes); see attn_fwd_tile_d128 for the buffer rotation.
+// k0/v0/k1/v1: four distinct __shared__ arrays of TILEB bytes.
 template <class T, class Prob>
 __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, float scale,
                                                    char* k0, char* v0, char* k1, char* v1) {
   using S = FwdShapeD256;
-  constexpr int D = S::D, DO = S::DO, BN = S::BN;
+  constexpr int D = S::D, BN = S::BN;
   const float scale_log2 = scale * kLog2e;
   constexpr float kLazy = 8.f;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
 
   const int nrows = P.nrows;
@@ -81,111 +71,75 @@ __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, floa
   }
 
   // Sᵀ operand of step c: row lr, logical chunk 2c + lh, stored at
-  // (2c + lh) ^ swz(lr) = 2c ^ (lh ^ swz(lr)), i.e. byte offset kbase ^ 32c.
-  int kbase = lr * S::KROWB + 16 * (lh ^ swz_chunk(lr));
-  // Vᵀ operand (as in attn_fwd_tile_d128, rows of VROWB bytes).
-  int voff[2][DO / 32];
+  // (2c + lh) ^ swz(lr) within its 256-byte half, i.e. byte offset
+  // kbase ^ 32c (bit 8 of 32c selects the half).  Vᵀ operand, 16-key chunk kc, d tile dt: lane k reads row 16kc +
+  // 4(k/32) + (k%16)/4 (+8 for the upper half), logical chunk 4dt + q with
+  // q = 2((k/16)%2) + (k%4)/2; stored at (4dt + q) ^ swz(row), i.e. byte
+  // offset vbase[hf] ^ 64dt.
+  int kbase = lr * S::ROWB + 16 * (lh ^ swz_chunk(lr));
+  int vbase[2];
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     const int r = 4 * (lane >> 5) + ((lane & 15) >> 2) + 8 * hf;
+    const int q = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
     const int sw = swz_chunk(r);
-#pragma unroll
-    for (int dt = 0; dt < DO / 32; ++dt) {
-      const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-      voff[hf][dt] = r * S::VROWB + 16 * (chunk ^ sw) + 8 * (lane & 1);
-    }
+    vbase[hf] = r * S::ROWB + 64 * (sw >> 2) + 16 * (q ^ (sw & 3)) + 8 * (lane & 1);
   }
 
-  auto visible = [&](int n0) { return wave_active && n0 < w_hi_max && n0 + BN > w_lo_min; };
-  f32x16 o[DO / 32];
-  f32x16 s;
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+    agpr_fence_in(o[dt]);
+  }
+  float ms_run = neg_inf(), l_run = 0.f;
+  bool o_live = false;  // wave-uniform: an O product has been issued
   u32x4 pb[BN / 16];
-  float ms_run, l_run;
-  int vcol = 0;  // first O / V column of the pass
   constexpr int kAheadS = FA_FWD_AHEAD_S, kAheadO = FA_FWD_AHEAD_O;
 
-  auto gemm_s = [&](const char* kb) {
-    asm volatile("" : "+v"(kbase));  // one base register, not one per step
+  auto visible = [&](int j) {
+    return wave_active && j * BN < w_hi_max && j * BN + BN > w_lo_min;
+  };
+  // acc = K Qᵀ for the tile in kb; extra(c) runs after the product of step c.
+  auto gemm_s = [&](f32x16& acc, const char* kb, auto extra) {
+    asm volatile("" : "+v"(kbase));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
     lds_pipeline<D / 16, kAheadS>(
         [&](int c) { return ld16(kb + (kbase ^ (32 * c))); },
-        [&](int c, const u32x4& k) { s = T::mma32(k, qf[c], s); });
-  };
-  auto softmax = [&](int n0) {
-    const bool need_mask = (n0 < w_lo_max) || (n0 + BN > w_hi_min);
-    if (need_mask) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kv = n0 + 8 * (i >> 2) + 4 * lh + (i & 3);
-        if (kv < my_lo || kv >= my_hi) s[i] = neg_inf();
-      }
-    }
-    float mt = neg_inf();
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[i]);
-    mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
-    const bool grow = mt > ms_run + kLazy;
-    if (__any(grow)) {
-      const float ms_new = grow ? mt : ms_run;
-      const float alpha = grow ? fast_exp2(ms_run - ms_new) : 1.f;
-      ms_run = ms_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DO / 32; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-    }
-    const float mb = ms_run == neg_inf() ? 0.f : ms_run;
-#pragma unroll
-    for (int kc = 0; kc < BN / 16; ++kc)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int e = 8 * kc + 2 * w;
-        const float p0 = fast_exp2(fmaf(s[e], scale_log2, -mb));
-        const float p1 = fast_exp2(fmaf(s[e + 1], scale_log2, -mb));
-        pb[kc][w] = T::pack(p0, p1);
-        l_run = T::sum2(p0, p1, pb[kc][w], l_run);
-      }
+        [&](int c, const u32x4& k) {
+          acc = T::mma32(k, qf[c], acc);
+          extra(c);
+        });
   };
   auto gemm_o = [&](const char* vb) {
+    asm volatile("" : "+v"(vbase[0]), "+v"(vbase[1]));
     struct VOps {
       u32x2 lo, hi;
     };
-    lds_pipeline<(BN / 16) * (DO / 32), kAheadO>(
+    lds_pipeline<(BN / 16) * (D / 32), kAheadO>(
         [&](int k) {
-          const int kc = k / (DO / 32), dt = k % (DO / 32);
-          return VOps{lds_read_tr(vb + voff[0][dt] + kc * 16 * S::VROWB),
-                      lds_read_tr(vb + voff[1][dt] + kc * 16 * S::VROWB)};
+          const int kc = k / (D / 32), dt = k % (D / 32);
+          const int ro = kc * 16 * S::ROWB;
+          return VOps{lds_read_tr(vb + (vbase[0] ^ (64 * dt)) + ro),
+                      lds_read_tr(vb + (vbase[1] ^ (64 * dt)) + ro)};
         },
         [&](int k, const VOps& r) {
-          const int kc = k / (DO / 32), dt = k % (DO / 32);
-          const u32x4 a = {r.lo[0], r.lo[1], r.hi[0], r.hi[1]};
-          o[dt] = T::mma32(a, pb[kc], o[dt]);
+          const int kc = k / (D / 32), dt = k % (D / 32);
+          mma32_agpr<T>(o[dt], u32x4{r.lo[0], r.lo[1], r.hi[0], r.hi[1]}, pb[kc]);
         });
   };
 
-  const bool grp_b = wave >= S::NW / 2;
-  const int j0 = max(wg_lo, 0) / BN;
-  const int j1 = (wg_hi + BN - 1) / BN;
-  // DMA (group A, wave w < 4): keys n0 + 8w .. n0 + 8w + 7 of K (four 1 KB
-  // blocks of 2 rows) and of the pass's V columns (two 1 KB blocks of 4
-  // rows).  Lane offsets are relative to the wave's first row and fixed;
-  // rows at or past wg_hi read as zero.
-  constexpr int KB = 4, VB = 2;  // 1 KB blocks per DMA wave
-  uint32_t k_loff[KB], v_loff[VB];
+  // DMA: wave w fills rows 8w .. 8w + 7 of a K or V tile (blocks 4w .. 4w+3,
+  // two rows per 1 KB block); lane offsets are fixed, rows at or past wg_hi
+  // read as zero.
+  uint32_t k_loff[4], v_loff[4];
 #pragma unroll
-  for (int ii = 0; ii < KB; ++ii) {
+  for (int ii = 0; ii < 4; ++ii) {
     const int r8 = 2 * ii + (lane >> 5);
-    const int r = 8 * wave + r8;  // row of the tile
-    const uint32_t c = (lane & 31) ^ swz_chunk(r);
+    const uint32_t c = (lane & 31) ^ swz_chunk(8 * wave + r8);
     k_loff[ii] = 2u * ((uint32_t)r8 * (uint32_t)P.k_row_stride() + 8u * c);
-  }
-#pragma unroll
-  for (int ii = 0; ii < VB; ++ii) {
-    const int r8 = 4 * ii + (lane >> 4);
-    const int r = 8 * wave + r8;
-    const uint32_t c = (lane & 15) ^ swz_chunk(r);
     v_loff[ii] = 2u * ((uint32_t)r8 * (uint32_t)P.v_row_stride() + 8u * c);
   }
   auto issue_rows = [&](int n0, char* dst, auto is_v) {
@@ -193,35 +147,14 @@ __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, floa
     const int nw = n0 + 8 * wave;
     const int nvalid = min(8, wg_hi - nw);  // n0 < wg_hi, so n0's row resolves
     const int nb = nvalid > 0 ? nw : n0;
-    const uint16_t* base = kV ? P.v_ptr(nb) + vcol : P.k_ptr(nb);
-    // K rows are read whole, V rows one pass's DO columns from vcol.
-    const uint32_t bytes =
-        span_bytes(nvalid, kV ? P.v_row_stride() : P.k_row_stride(), kV ? DO : D);
+    const uint16_t* base = kV ? P.v_ptr(nb) : P.k_ptr(nb);
+    const uint32_t bytes = span_bytes(nvalid, kV ? P.v_row_stride() : P.k_row_stride(), D);
     u32x4 rs = rsrc_words(base, bytes);
 #pragma unroll
     for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(rs[w]);
-    if constexpr (kV) {
 #pragma unroll
-      for (int ii = 0; ii < VB; ++ii)
-        buffer_lds16_opaque(rs, v_loff[ii], dst + (VB * wave + ii) * 1024);
-    } else {
-#pragma unroll
-      for (int ii = 0; ii < KB; ++ii)
-        buffer_lds16_opaque(rs, k_loff[ii], dst + (KB * wave + ii) * 1024);
-    }
-  };
-  auto issue_k = [&](int n0, char* kb) { issue_rows(n0, kb, BoolC<false>{}); };
-  auto issue_v = [&](int n0, char* vb) { issue_rows(n0, vb, BoolC<true>{}); };
-  auto mma_phase = [&](int j, const char* vprev, const char* kcur, char* knext, char* vcur,
-                       auto dma) {
-    constexpr bool kDma = decltype(dma)::value;
-    if (j - 1 >= j0 && visible((j - 1) * BN)) gemm_o(vprev);
-    if (kDma && j + 1 < j1) issue_k((j + 1) * BN, knext);
-    if (j < j1 && visible(j * BN)) gemm_s(kcur);
-    if (kDma && j < j1) issue_v(j * BN, vcur);
-  };
-  auto sm_phase = [&](int js) {
-    if (js >= j0 && js < j1 && visible(js * BN)) softmax(js * BN);
+    for (int ii = 0; ii < 4; ++ii)
+      buffer_lds16_opaque(rs, kV ? v_loff[ii] : k_loff[ii], dst + (4 * wave + ii) * 1024);
   };
   auto tile_barrier = [&]() {
     __builtin_amdgcn_sched_barrier(0);
@@ -229,42 +162,97 @@ __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, floa
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto run = [&](auto group_b) {
-    constexpr bool kB = decltype(group_b)::value;
-    constexpr BoolC<!kB> dma{};
-    for (int j = j0;; j += 2) {
-      if (kB) sm_phase(j - 1); else mma_phase(j, v1, k0, k1, v0, dma);
-      if (kB) mma_phase(j, v1, k0, k1, v0, dma); else sm_phase(j);
-      tile_barrier();
-      if (j + 1 > j1) break;
-      if (kB) sm_phase(j); else mma_phase(j + 1, v0, k1, k0, v1, dma);
-      if (kB) mma_phase(j + 1, v0, k1, k0, v1, dma); else sm_phase(j + 1);
-      tile_barrier();
-      if (j + 2 > j1) break;
+
+  // Iteration j: K(j + 1) in kn, V(j) in vc; DMA of K(j + 2) into kd and of
+  // V(j + 1) into vd; cur holds Sᵀ(j), nxt receives Sᵀ(j + 1).
+  const int j0 = max(wg_lo, 0) / BN;
+  const int j1 = (wg_hi + BN - 1) / BN;
+  auto step = [&](int j, const char* kn, const char* vc, char* kd, char* vd, f32x16& cur,
+                  f32x16& nxt) {
+    tile_barrier();
+    if (j + 2 < j1) issue_rows((j + 2) * BN, kd, BoolC<false>{});
+    if (j + 1 < j1) issue_rows((j + 1) * BN, vd, BoolC<true>{});
+    const bool vis = visible(j);
+    const bool vis_n = j + 1 < j1 && visible(j + 1);
+    if (!vis) {
+      if (vis_n) gemm_s(nxt, kn, [](int) {});
+      return;
     }
+    const int n0 = j * BN;
+    if ((n0 < w_lo_max) || (n0 + BN > w_hi_min)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kv = n0 + 8 * (i >> 2) + 4 * lh + (i & 3);
+        if (kv < my_lo || kv >= my_hi) cur[i] = neg_inf();
+      }
+    }
+    // The online-softmax update of tile j in 14 slices: row max (steps
+    // 0-3), the other half-row's max (4), rescale decision (5), then one
+    // pair of probabilities per step (6-13).
+    float mt = neg_inf(), alpha = 1.f, mb = 0.f;
+    bool grow = false;
+    auto slice = [&](int c) {
+      if (c < 4) {
+#pragma unroll
+        for (int i = 4 * c; i < 4 * c + 4; ++i) mt = fmaxf(mt, cur[i]);
+      } else if (c == 4) {
+        mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+      } else if (c == 5) {
+        // A row's max only moves when the tile max exceeds it by more than
+        // kLazy, so P <= 2^kLazy and O is rescaled on few tiles.
+        grow = mt > ms_run + kLazy;
+        const float ms_new = grow ? mt : ms_run;
+        alpha = grow ? fast_exp2(ms_run - ms_new) : 1.f;
+        ms_run = ms_new;
+        l_run *= alpha;
+        // A row with no visible key so far has ms_run = -inf and only -inf
+        // scores in this tile: any finite offset gives P = 0.
+        mb = ms_run == neg_inf() ? 0.f : ms_run;
+      } else if (c < 14) {
+        const int pr = c - 6, e = 2 * pr;
+        const float p0 = fast_exp2(fmaf(cur[e], scale_log2, -mb));
+        const float p1 = fast_exp2(fmaf(cur[e + 1], scale_log2, -mb));
+        pb[pr >> 2][pr & 3] = T::pack(p0, p1);
+        l_run = T::sum2(p0, p1, pb[pr >> 2][pr & 3], l_run);
+      }
+    };
+    if (vis_n) {
+      gemm_s(nxt, kn, slice);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 14; ++c) slice(c);
+    }
+    if (o_live && __any(grow)) {
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        agpr_fence_out(o[dt]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+      }
+    }
+    gemm_o(vc);
+    o_live = true;
   };
 
-  // Every wave runs both passes (their barriers pair up); the last barrier
-  // of a pass also frees the buffers for the next pass's first DMA.
-#pragma unroll 1
-  for (int pass = 0; pass < S::NPASS; ++pass) {
-    vcol = pass * DO;
-#pragma unroll
-    for (int dt = 0; dt < DO / 32; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-    ms_run = neg_inf();
-    l_run = 0.f;
-    if (j0 < j1 && !grp_b) issue_k(j0 * BN, k0);
-    wait_vmem();
-    __syncthreads();
-    if (grp_b)
-      run(BoolC<true>{});
-    else
-      run(BoolC<false>{});
-    const float l_all = l_run + swap_halves(l_run);
-    if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run, vcol);
+  if (j0 < j1) {
+    f32x16 sa, sb;
+    issue_rows(j0 * BN, k0, BoolC<false>{});
+    tile_barrier();
+    if (j0 + 1 < j1) issue_rows((j0 + 1) * BN, k1, BoolC<false>{});
+    issue_rows(j0 * BN, v0, BoolC<true>{});
+    if (visible(j0)) gemm_s(sa, k0, [](int) {});
+    for (int j = j0;; j += 2) {
+      step(j, k1, v0, k0, v1, sa, sb);
+      if (j + 1 >= j1) break;
+      step(j + 1, k0, v1, k1, v0, sb, sa);
+      if (j + 2 >= j1) break;
+    }
   }
+
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) agpr_fence_out(o[dt]);
+  const float l_all = l_run + swap_halves(l_run);
+  if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
 }
 
 }  // namespace fa

@@ -25,14 +25,15 @@ constexpr int kFwd128Keys = 64;
 constexpr int kFwd128Waves = 8;
 
 // ---- dense / paged forward, head_dim 256 (fa_fwd_d256.h)
-// The head_dim 128 schedule with 32-key tiles and O in two 128-column passes
-// (the scores recomputed), so two waves fit each SIMD (230 VGPRs, no
-// spills).  Evidence: T1 shape at head_dim 256 (B=2, S=8192, H=8, causal)
-// 0.844 ms against 1.204 ms for the one-pass 4-wave core (406 registers,
-// one wave per SIMD), despite 1.5x the matrix products.
-constexpr int kFwd256Rows = 256;
-constexpr int kFwd256Keys = 32;
-constexpr int kFwd256Waves = 8;
+// 4 waves x 32 rows, one wave per SIMD, one pass over 32-key tiles with O in
+// AGPRs (256 VGPRs + 155 AGPRs, no spills).  Evidence, T1 shape at head_dim
+// 256 (B=2, S=8192, H=8, causal), same box: 0.638-0.649 ms against
+// 0.760-0.763 ms for 8 waves x 32 rows at two waves per SIMD (230 VGPRs, O in
+// two 128-column passes with the scores recomputed, 1.5x the products),
+// bit-identical outputs; that schedule in turn took 0.844 ms against 1.204 ms
+// for the one-pass register-staged 4-wave core (406 registers, accumulators
+// shuffled between the register files).
+constexpr int kFwd256Rows = 128;
 
 // ---- forward, head_dim 64 / 256 / 512 (fa_fwd_core.h; head_dim 256 only for
 // paged problems with pages of fewer than 16 keys)
