@@ -111,7 +111,7 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) part = T::dot2(ov[w], df[c][w], part);
     }
-    const float full = part + __shfl_xor(part, 32);
+    const float full = half_sum(part);
     if (row_valid) {
       const float l = a.lse[(int64_t)bh * Sq + row];
       lse2 = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;

@@ -162,9 +162,29 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
-// Exchange with the lane 32 positions away (lane ^ 32).
-__device__ __forceinline__ float swap_halves(float x) {
-  return __shfl_xor(x, 32);
+// max / sum of x over lanes l and l ^ 32, in registers (no LDS round trip,
+// whose lgkmcnt wait would also wait for LDS operand reads in flight).
+// v_permlane32_swap swaps the upper 32 lanes of its first operand with the
+// lower 32 lanes of its second; with x in both, lane l of the two results
+// holds x[l] and x[l ^ 32], in an order that depends on the half, so only
+// order-independent combinations are formed.  Inline assembly: the
+// compiler folds the builtin's two results into one when both inputs are
+// the same value.  `s_nop 1`: a VALU write of either operand needs 2 wait
+// states before the swap reads it.
+__device__ __forceinline__ void half_pair(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float half_max(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return a + b;
 }
 
 __device__ __forceinline__ u32x4 ld16(const void* p) {

@@ -444,7 +444,7 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
   };
   auto finish_item = [&]() {
     float lt = lsum + __shfl_xor(lsum, 16);
-    lt += __shfl_xor(lt, 32);
+    lt = half_sum(lt);
     if (l16 < GB) {
       const int h = cit.hk * G + cit.hg * GB + l16;
       const int64_t row = ((int64_t)cit.b * a.num_heads + h) * ws.nsplit + cit.c;
@@ -471,7 +471,7 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
       mt = fmaxf(mt, s[i]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32)) * scale_log2;
+    mt = half_max(mt) * scale_log2;
     const bool grow = mt > ms + 8.f;
     if (__any(grow)) {
       const float ms_new = grow ? mt : ms;

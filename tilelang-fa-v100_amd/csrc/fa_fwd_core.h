@@ -208,7 +208,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
         for (int kt = 0; kt < S::KT; ++kt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kt][i]);
-        mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+        mt = half_max(mt) * scale_log2;
         const bool grow = mt > ms_run + kLazy;
         if (__any(grow)) {
           const float ms_new = grow ? mt : ms_run;
@@ -254,7 +254,7 @@ __device__ __forceinline__ void attn_fwd_tile(const Prob& P, int row0,
 
   // Epilogue: both halves of the wave hold partial sums of the same row.
   // (No early return: a second pass still takes part in the barriers.)
-  const float l_all = l_run + swap_halves(l_run);
+  const float l_all = half_sum(l_run);
   if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run, vcol);
   }  // pass
 }

@@ -174,7 +174,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128_plain(const Prob& P, int row0
     for (int kt = 0; kt < BN / 32; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kt][i]);
-    mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+    mt = half_max(mt) * scale_log2;
     const bool grow = mt > ms_run + kLazy;
     if (__any(grow)) {
       const float ms_new = grow ? mt : ms_run;
@@ -226,7 +226,7 @@ __device__ __forceinline__ void attn_fwd_tile_d128_plain(const Prob& P, int row0
     compute_tile((j + 1) * BN, k1, v1);
   }
 
-  const float l_all = l_run + swap_halves(l_run);
+  const float l_all = half_sum(l_run);
   if (!row_valid) return;
   fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
 }
@@ -417,7 +417,7 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
     for (int kt = 0; kt < BN / 32; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kt][i]);
-    mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+    mt = half_max(mt) * scale_log2;
     const bool grow = mt > ms_run + kLazy;
     if (__any(grow)) {
       const float ms_new = grow ? mt : ms_run;
@@ -530,7 +530,7 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
     run(BoolC<false>{});
 
   // Every wave is past the loop's last barrier: LDS and qf are free.
-  const float l_all = l_run + swap_halves(l_run);
+  const float l_all = half_sum(l_run);
   if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
   if (!next(P, row0)) break;
   start_tile();

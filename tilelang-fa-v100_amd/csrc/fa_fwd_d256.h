@@ -196,7 +196,7 @@ __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, floa
 #pragma unroll
         for (int i = 4 * c; i < 4 * c + 4; ++i) mt = fmaxf(mt, cur[i]);
       } else if (c == 4) {
-        mt = fmaxf(mt, swap_halves(mt)) * scale_log2;
+        mt = half_max(mt) * scale_log2;
       } else if (c == 5) {
         // A row's max only moves when the tile max exceeds it by more than
         // kLazy, so P <= 2^kLazy and O is rescaled on few tiles.
@@ -251,7 +251,7 @@ __device__ __forceinline__ void attn_fwd_tile_d256(const Prob& P, int row0, floa
 
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) agpr_fence_out(o[dt]);
-  const float l_all = l_run + swap_halves(l_run);
+  const float l_all = half_sum(l_run);
   if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
 }
 
