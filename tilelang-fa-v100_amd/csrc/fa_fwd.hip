@@ -32,6 +32,7 @@ struct DenseRows {
   // K / V rows are a base plus a row stride (below 2^24 elements, checked
   // by the launcher), so whole tiles can be DMA'd through buffer resources.
   static constexpr bool kF32Out = false;
+  static constexpr bool kRowStrided = true;  // k_ptr(n + m) = k_ptr(n) + m * ks
 
   // Row r sees keys [r + off - wl, r + off + wr] within [0, sk).
   __device__ int kv_lo(int r) const { return wl >= 0 ? min(max(r + off - wl, 0), sk) : 0; }
@@ -64,7 +65,7 @@ struct FwdKernelCfg<256, true> {
   static constexpr int THREADS = 64 * FwdShapeD256::NW;
   static constexpr int WAVES_PER_EU = 1;
   static constexpr int WG_PER_CU = 1;
-  static constexpr int LDS_BYTES = 4 * FwdShapeD256::TILEB;
+  static constexpr int LDS_BYTES = 5 * FwdShapeD256::TILEB;
 };
 template <bool PP>
 struct FwdKernelCfg<128, PP> {
@@ -91,8 +92,8 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
       attn_fwd_tile_d128_plain<T>(P, row0, scale, k0, v0, k1, v1);
   } else if constexpr (D == 256 && PP) {
     constexpr int B = FwdShapeD256::TILEB;
-    __shared__ __attribute__((aligned(16))) char k0[B], v0[B], k1[B], v1[B];
-    attn_fwd_tile_d256<T>(P, row0, scale, k0, v0, k1, v1);
+    __shared__ __attribute__((aligned(16))) char smem[5 * B];
+    attn_fwd_tile_d256<T>(P, row0, scale, smem);
   } else {
     __shared__ __attribute__((aligned(16))) uint16_t smem[FwdShape<D>::LDS_ELEMS];
     attn_fwd_tile<T, D>(P, row0, scale, smem);
@@ -195,6 +196,7 @@ struct PagedRows {
   int G, nrows, seq_len, prefix, wq, wk;
   bool causal, has_lse;
   static constexpr bool kF32Out = false;
+  static constexpr bool kRowStrided = false;
 
   __device__ int kv_lo(int r) const {
     if (!causal || wq <= 0) return 0;
