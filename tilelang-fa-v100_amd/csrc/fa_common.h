@@ -399,33 +399,6 @@ __device__ __forceinline__ void buffer_lds16_opaque(u32x4 rsrc, uint32_t voff, c
       : "v"(voff), "s"(rsrc), "s"(lds_addr(lds_block))
       : "memory");
 }
-// Four buffer_lds16 DMAs into the consecutive 1 KB blocks from lds_block,
-// block i at lane offset voff[i]: one save and restore of M0 for the four.
-__device__ __forceinline__ void buffer_lds16x4_opaque(u32x4 rsrc, const uint32_t (&voff)[4],
-                                                      char* lds_block) {
-  uint32_t saved;
-  const uint32_t l0 = lds_addr(lds_block);
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %6\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
-      "s_mov_b32 m0, %7\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
-      "s_mov_b32 m0, %8\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
-      "s_mov_b32 m0, %9\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %4, %5, 0 offen lds\n\t"
-      "s_nop 0\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(rsrc), "s"(l0),
-        "s"(l0 + 1024), "s"(l0 + 2048), "s"(l0 + 3072)
-      : "memory");
-}
 __device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_block) {
   uint32_t saved;
   asm volatile(

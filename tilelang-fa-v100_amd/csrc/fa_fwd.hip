@@ -14,7 +14,7 @@
 
 #include "fa_fwd_core.h"
 #include "fa_fwd_d128.h"
-#include "fa_fwd_d256.h"
+#include "fa_fwd_1w.h"
 #include "fa_internal.h"
 
 namespace fa {
@@ -59,14 +59,18 @@ struct FwdKernelCfg {
   static constexpr int WG_PER_CU = WAVES_PER_EU;  // 4 waves: one per SIMD each
   static constexpr int LDS_BYTES = FwdShape<D>::LDS_ELEMS * 2;
 };
-template <>
-struct FwdKernelCfg<256, true> {
-  static constexpr int BM = FwdShapeD256::BM;
-  static constexpr int THREADS = 64 * FwdShapeD256::NW;
+// One-wave-per-SIMD cores (fa_fwd_1w.h).
+template <int D, int RB>
+struct FwdKernelCfg1W {
+  using S = FwdShape1W<D, RB>;
+  static constexpr int BM = S::BM;
+  static constexpr int THREADS = 64 * S::NW;
   static constexpr int WAVES_PER_EU = 1;
   static constexpr int WG_PER_CU = 1;
-  static constexpr int LDS_BYTES = 5 * FwdShapeD256::TILEB;
+  static constexpr int LDS_BYTES = 5 * S::TILEB;
 };
+template <>
+struct FwdKernelCfg<256, true> : FwdKernelCfg1W<256, 1> {};
 template <bool PP>
 struct FwdKernelCfg<128, PP> {
   static constexpr int BM = FwdShapeD128::BM;
@@ -91,9 +95,8 @@ __device__ __forceinline__ void run_fwd_tile(const Prob& P, int row0, float scal
     else
       attn_fwd_tile_d128_plain<T>(P, row0, scale, k0, v0, k1, v1);
   } else if constexpr (D == 256 && PP) {
-    constexpr int B = FwdShapeD256::TILEB;
-    __shared__ __attribute__((aligned(16))) char smem[5 * B];
-    attn_fwd_tile_d256<T>(P, row0, scale, smem);
+    __shared__ __attribute__((aligned(16))) char smem[FwdKernelCfg1W<256, 1>::LDS_BYTES];
+    attn_fwd_tile_1w<T, 256, 1>(P, row0, scale, smem);
   } else {
     __shared__ __attribute__((aligned(16))) uint16_t smem[FwdShape<D>::LDS_ELEMS];
     attn_fwd_tile<T, D>(P, row0, scale, smem);

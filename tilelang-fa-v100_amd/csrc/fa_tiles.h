@@ -24,7 +24,7 @@ constexpr int kFwd128Rows = 256;
 constexpr int kFwd128Keys = 64;
 constexpr int kFwd128Waves = 8;
 
-// ---- dense / paged forward, head_dim 256 (fa_fwd_d256.h)
+// ---- dense / paged forward, head_dim 256 (fa_fwd_1w.h)
 // 4 waves x 32 rows, one wave per SIMD, one pass over 32-key tiles with O in
 // AGPRs (256 VGPRs + 155 AGPRs, no spills).  Evidence, T1 shape at head_dim
 // 256 (B=2, S=8192, H=8, causal), same box: 0.638-0.649 ms against
