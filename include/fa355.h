@@ -96,8 +96,13 @@ typedef struct fa_fwd_args {
 int fa_fwd(const fa_fwd_args* args, void* stream);
 
 /* Backward: LSE-recompute FlashAttention-2 gradient.  dq/dk/dv use the same
- * layout rules as q/k/v.  Workspace holds the per-row statistics (LSE and
- * dot(O, dO)); its size comes from fa_bwd_workspace_bytes. */
+ * layout rules as q/k/v.  The workspace holds the per-row statistics (LSE and
+ * dot(O, dO)) and, at head_dim 128 with causal or full attention, the 16-bit
+ * dS tiles from which dq is formed (2 bytes per (query, key) pair the mask
+ * lets through, up to 4 GiB); fa_bwd_workspace_bytes gives that size.  A
+ * workspace of at least fa_bwd_min_workspace_bytes (the statistics only)
+ * selects the path that recomputes S and dP for dq instead; both paths are
+ * deterministic. */
 typedef struct fa_bwd_args {
   const void* q;
   const void* k;
@@ -127,8 +132,8 @@ typedef struct fa_bwd_args {
   int32_t dtype;
   int32_t deterministic; /* accepted and ignored, as in the reference
                           * (interface.py:16-17): the backward has no atomics
-                          * (a query-stationary kernel writes each dq row
-                          * once), so dq, dk and dv always repeat bit for bit,
+                          * (each dq row is summed by one wave in a fixed
+                          * order), so dq, dk and dv always repeat bit for bit,
                           * like the reference's kernels
                           * (_kernels_backward.py:10-85,88-176) */
   int32_t has_window;    /* as in fa_fwd_args */
@@ -138,6 +143,10 @@ typedef struct fa_bwd_args {
 
 /* Replaces tilelang_backward (_kernels_backward.py:200-208). */
 size_t fa_bwd_workspace_bytes(const fa_bwd_args* args);
+/* No counterpart in the reference (its backward allocates its own row_dot
+ * buffer, _kernels_backward.py:203): the smallest workspace fa_bwd accepts,
+ * for callers that trade the dS tiles' memory for recomputing S and dP. */
+size_t fa_bwd_min_workspace_bytes(const fa_bwd_args* args);
 int fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes,
            void* stream);
 

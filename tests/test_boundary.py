@@ -128,11 +128,15 @@ def test_bwd_workspace_size_and_checks():
     lib = _lib.load()
     a = bwd_args()
     rows = 4 * 2048 * 16
-    # the row statistics only (no dQ accumulator), whatever head_dim / `deterministic`
+    stats = 2 * rows * 4 + 256
+    # the row statistics (no dQ accumulator), whatever head_dim / `deterministic`;
+    # at head_dim 128 also the dS tiles (causal: 64 * 65 / 2 tiles per head)
     for hd in (64, 128, 256):
         for det in (0, 1):
             ad = bwd_args(head_dim=hd, deterministic=det)
-            assert lib.fa_bwd_workspace_bytes(ctypes.byref(ad)) == 2 * rows * 4 + 256
+            assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(ad)) == stats
+            ds = 2048 * 4 * 16 * (64 * 65 // 2) if hd == 128 else 0
+            assert lib.fa_bwd_workspace_bytes(ctypes.byref(ad)) == (stats + ds if ds else stats)
     # workspace missing / too small is rejected before any launch
     assert lib.fa_bwd(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE
     assert lib.fa_bwd(ctypes.byref(a), 0x4000, 16, None) == _lib.FA_E_WORKSPACE
@@ -143,6 +147,56 @@ def test_bwd_workspace_size_and_checks():
     big = bwd_args(batch=4096, num_heads=16, num_heads_k=16, seqlen_q=16, seqlen_k=16)
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(big)) == 0
     assert b"65535" in lib.fa_last_error_message()
+
+
+def _ds_tiles_brute(sq, sk, causal):
+    """(query tile, key block) pairs of 32 x 32 that a causal (j <= i + sk - sq)
+    or full mask reaches: the dS tiles the dK / dV kernel stores."""
+    nq, nk = -(-sq // 32), -(-sk // 32)
+    if not causal:
+        return nq * nk
+    return sum(1 for qt in range(nq) for kb in range(nk) if 32 * kb <= 32 * qt + 31 + sk - sq)
+
+
+@pytest.mark.parametrize("sq,sk", [(1, 1), (31, 33), (33, 31), (64, 4096), (4096, 64),
+                                   (2048, 2048), (1000, 777), (777, 1000), (96, 97), (5, 300),
+                                   (300, 5)])
+@pytest.mark.parametrize("causal", [0, 1])
+def test_bwd_ds_tile_count(sq, sk, causal):
+    """The dS workspace holds exactly one 2 KB tile per reachable 32 x 32 pair
+    (closed-form prefix sums of the kernels against a brute-force count)."""
+    lib = _lib.load()
+    a = bwd_args(batch=3, num_heads=5, num_heads_k=5, seqlen_q=sq, seqlen_k=sk, causal=causal)
+    for n in ("q", "o", "do", "dq"):
+        getattr(a, f"{n}_stride")[:] = (sq * 5 * 128, 5 * 128, 128)
+    for n in ("k", "v", "dk", "dv"):
+        getattr(a, f"{n}_stride")[:] = (sk * 5 * 128, 5 * 128, 128)
+    stats = 2 * 3 * 5 * sq * 4 + 256
+    assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(a)) == stats
+    off = -(-stats // 256) * 256
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == \
+        off + 2048 * 15 * _ds_tiles_brute(sq, sk, causal)
+    # a window band keeps the recompute path (statistics only)
+    a.has_window, a.window_left, a.window_right = 1, 40, 0
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == stats
+
+
+def test_bwd_ds_workspace_cap():
+    """dS tiles beyond 4 GiB: the workspace falls back to the statistics."""
+    lib = _lib.load()
+    s = 32768
+    a = bwd_args(batch=1, num_heads=8, num_heads_k=8, seqlen_q=s, seqlen_k=s, causal=1)
+    for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv"):
+        getattr(a, f"{n}_stride")[:] = (s * 8 * 128, 8 * 128, 128)
+    stats = 2 * 8 * s * 4 + 256
+    per_head = 1024 * 1025 // 2  # 1.07 GB of dS per head
+    assert 2048 * 8 * per_head > 4 << 30
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == stats
+    a.num_heads = a.num_heads_k = 3  # 3.2 GB: under it
+    for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv"):
+        getattr(a, f"{n}_stride")[:] = (s * 3 * 128, 3 * 128, 128)
+    stats = 2 * 3 * s * 4 + 256
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == stats + 2048 * 3 * per_head
 
 
 def paged_args(**over):

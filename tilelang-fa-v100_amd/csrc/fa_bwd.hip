@@ -25,7 +25,12 @@
 //                       tiles of every query head that shares the KV head
 //                       (GQA).  K and V of the wave stay in registers.
 //   bwd_main_mfma_kernel  head_dim 128 / 256 dK / dV (fa_bwd_mfma.h).
+// At head_dim 128 with causal or full attention and a workspace of
+// bwd_workspace_bytes, the order is instead bwd_stats_kernel (the row
+// statistics), bwd_main_mfma_kernel<..., DS = true> (dK / dV, storing its dS
+// tiles) and bwd_dq_ds_kernel (dQ = scale · dS K from them), fa_bwd_ds.h.
 #include "fa_bwd_dq.h"
+#include "fa_bwd_ds.h"
 #include "fa_bwd_mfma.h"
 #include "fa_common.h"
 #include "fa_internal.h"
@@ -274,26 +279,62 @@ __global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const f
 
 // ----------------------------------------------------------------- launchers
 
-// Workspace: the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot).
-size_t bwd_workspace_bytes(const fa_bwd_args& a) {
+// Workspace: the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot), then,
+// for the dS-store path, the dS tiles (fa_bwd_ds.h) from byte ds_offset(a).
+static size_t stats_bytes(const fa_bwd_args& a) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
   return 2 * rows * sizeof(float) + 256;
 }
+static size_t ds_offset(const fa_bwd_args& a) { return (stats_bytes(a) + 255) & ~(size_t)255; }
 
-// Key-stationary dK / dV kernel for one mask mode.
+// Bytes of dS tiles for the dS-store path, or 0 where it does not apply:
+// head_dim 128, causal or full attention, at most tiles::kBwdDsMaxBytes.
+static size_t ds_bytes(const fa_bwd_args& a) {
+  const int mode = mask_mode(a);
+  if (a.head_dim != 128 || mode == kMaskBand || a.seqlen_q <= 0 || a.seqlen_k <= 0) return 0;
+  const DsTiles L = mode == kMaskCausal ? ds_tiles<kMaskCausal>(a.seqlen_q, a.seqlen_k)
+                                        : ds_tiles<kMaskNone>(a.seqlen_q, a.seqlen_k);
+  const size_t bytes = 2048 * (size_t)a.batch * a.num_heads * (size_t)L.per_head();
+  return bytes <= tiles::kBwdDsMaxBytes ? bytes : 0;
+}
+
+size_t bwd_min_workspace_bytes(const fa_bwd_args& a) { return stats_bytes(a); }
+
+size_t bwd_workspace_bytes(const fa_bwd_args& a) {
+  const size_t ds = ds_bytes(a);
+  return ds ? ds_offset(a) + ds : stats_bytes(a);
+}
+
+// Key-stationary dK / dV kernel for one mask mode; with ds, also stores the
+// dS tiles (head_dim 128, causal or full attention).
 template <class T, int D>
-static void launch_bwd_main(const fa_bwd_args& a, int mode, const float* stats, hipStream_t st) {
+static void launch_bwd_main(const fa_bwd_args& a, int mode, const float* stats, uint16_t* ds,
+                            hipStream_t st) {
   if constexpr (D >= 128) {
     using S = BwdShapeMfma<D>;
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S::NW);
     if (kvtiles == 0) return;  // no keys: dK / dV are empty
+    if constexpr (D == 128) {
+      if (ds) {
+        if (mode == kMaskCausal)
+          hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal, true>), grid, block, 0, st,
+                             a, stats, ds);
+        else
+          hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone, true>), grid, block, 0, st, a,
+                             stats, ds);
+        return;
+      }
+    }
     if (mode == kMaskCausal)
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal>), grid, block, 0, st, a, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal>), grid, block, 0, st, a, stats,
+                         nullptr);
     else if (mode == kMaskBand)
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand>), grid, block, 0, st, a, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskBand>), grid, block, 0, st, a, stats,
+                         nullptr);
     else
-      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
+      hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats,
+                         nullptr);
   } else {
     using S = BwdShape<D>;
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
@@ -322,32 +363,59 @@ static void launch_bwd_dq(const fa_bwd_args& a, int mode, float* stats, hipStrea
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
 }
 
+// dS-store path (head_dim 128): row statistics, dK / dV storing dS, then
+// dQ = scale · dS K.
+template <class T>
+static hipError_t launch_bwd_ds(const fa_bwd_args& a, int mode, void* ws, hipStream_t st) {
+  float* stats = static_cast<float*>(ws);
+  uint16_t* ds = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + ds_offset(a));
+  const int64_t waves = (int64_t)a.batch * a.num_heads * ((a.seqlen_q + 31) / 32);
+  hipLaunchKernelGGL((bwd_stats_kernel<T, 128>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     st, a, stats);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  launch_bwd_main<T, 128>(a, mode, stats, ds, st);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int nqb = ((a.seqlen_q + 31) / 32 + 7) / 8;
+  const dim3 grid((unsigned)nqb * a.num_heads * a.batch), block(512);
+  if (mode == kMaskCausal)
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, kMaskCausal>), grid, block, 0, st, a, ds);
+  else
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, kMaskNone>), grid, block, 0, st, a, ds);
+  return hipGetLastError();
+}
+
 // dQ (and the row statistics), then dK / dV.  Every output element is
-// produced by one fixed sequence of operations.
+// produced by one fixed sequence of operations.  A workspace of
+// bwd_workspace_bytes selects the dS-store path where it applies; one of
+// bwd_min_workspace_bytes, the recompute path.
 template <class T, int D>
-static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, hipStream_t st) {
-  float* stats = static_cast<float*>(ws);  // [B*H][2][Sq]
+static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const int mode = mask_mode(a);
+  if (D == 128 && ds_bytes(a) && ws_bytes >= bwd_workspace_bytes(a))
+    return launch_bwd_ds<T>(a, mode, ws, st);
+  float* stats = static_cast<float*>(ws);  // [B*H][2][Sq]
   launch_bwd_dq<T, D>(a, mode, stats, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch_bwd_main<T, D>(a, mode, stats, st);
+  launch_bwd_main<T, D>(a, mode, stats, nullptr, st);
   return hipGetLastError();
 }
 
 template <class T>
-static hipError_t launch_bwd_t(const fa_bwd_args& a, void* ws, hipStream_t st) {
+static hipError_t launch_bwd_t(const fa_bwd_args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   switch (a.head_dim) {
-    case 64: return launch_bwd_d<T, 64>(a, ws, st);
-    case 128: return launch_bwd_d<T, 128>(a, ws, st);
-    case 256: return launch_bwd_d<T, 256>(a, ws, st);
+    case 64: return launch_bwd_d<T, 64>(a, ws, ws_bytes, st);
+    case 128: return launch_bwd_d<T, 128>(a, ws, ws_bytes, st);
+    case 256: return launch_bwd_d<T, 256>(a, ws, ws_bytes, st);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_bwd(const fa_bwd_args& a, void* ws, hipStream_t st) {
-  return a.dtype == FA_DTYPE_BF16 ? launch_bwd_t<BFloat16>(a, ws, st)
-                                  : launch_bwd_t<Half>(a, ws, st);
+hipError_t launch_bwd(const fa_bwd_args& a, void* ws, size_t ws_bytes, hipStream_t st) {
+  return a.dtype == FA_DTYPE_BF16 ? launch_bwd_t<BFloat16>(a, ws, ws_bytes, st)
+                                  : launch_bwd_t<Half>(a, ws, ws_bytes, st);
 }
 
 }  // namespace fa

@@ -20,6 +20,7 @@
 #pragma once
 
 #include "fa355.h"
+#include "fa_bwd_ds.h"
 #include "fa_common.h"
 #include "fa_fwd_d128.h"
 
@@ -48,9 +49,11 @@ struct TrOps {
 };
 
 // MODE (MaskMode): full attention, causal, or a window band from the arguments.
-template <class T, int D_, int MODE>
+// DS: also store every computed 32 x 32 dS block to `ds` (tile layout of
+// fa_bwd_ds.h; head_dim 128, causal or full attention) for bwd_dq_ds_kernel.
+template <class T, int D_, int MODE, bool DS = false>
 __global__ __launch_bounds__((64 * BwdShapeMfma<D_>::NW), (BwdShapeMfma<D_>::WPE))
-void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
+void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
   using S = BwdShapeMfma<D_>;
   constexpr bool CAUSAL = MODE != kMaskNone;  // some (query, key) pairs are outside the band
   constexpr int D = S::D;
@@ -188,6 +191,17 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
   const uint16_t* q_i = q_top;
   const uint16_t* o_i = o_top;
   const float* s_i = s_top;
+  // DS: the dS tile of the tile `step` computes next (same sweep order as
+  // the issue side), stepped back by count(it) tiles per query tile.
+  static_assert(!DS || (D == 128 && MODE != kMaskBand), "dS tiles: head_dim 128, causal or full");
+  DsTiles dsl{1, 1, 1};
+  uint16_t* ds_top = nullptr;
+  if constexpr (DS) {
+    dsl = ds_tiles<(MODE == kMaskCausal ? kMaskCausal : kMaskNone)>(Sq, Sk);
+    ds_top = ds + 1024 * ((int64_t)(b * H + hk * G) * dsl.per_head() +
+                          dsl.prefix(max(it1, 1) - 1) + kvw / 32);
+  }
+  uint16_t* ds_c = ds_top;
   auto issue_q = [&](int it, int qo, int oo, int so) {
     const int i0 = it * S::BQ;
     // Buffer resources over the tile's valid rows: rows at or past Sq read
@@ -225,8 +239,10 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
   };
 
   // S, dP, softmax, dV and dK for query tile `it` (no barrier).  qo, oo, so:
-  // offsets of its Q, dO and statistics tiles.
-  auto step = [&](int it, int qo, int oo, int so) {
+  // offsets of its Q, dO and statistics tiles.  Returns whether the wave
+  // stored a dS tile (DS: two global stores, the wave's newest memory
+  // operations).
+  auto step = [&](int it, int qo, int oo, int so) -> bool {
     const char* qb = smem + qo;
     const char* ob = smem + oo;
     const float* st = reinterpret_cast<const float*>(smem + so);
@@ -241,7 +257,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
     // BKV / BQ tiles per workgroup.
     const bool active =
         (MODE != kMaskCausal || band.any(i0, i0 + S::BQ - 1, kvw, kvw + 31)) && kvw < Sk;
-    if (!active) return;
+    if (!active) return false;
     f32x16 s, dp;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
@@ -305,6 +321,15 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
         pB[kq][w] = T::pack(s[e], s[e + 1]);
         sB[kq][w] = T::pack(dp[e], dp[e + 1]);
       }
+    if constexpr (DS) {
+      // Chunk kq of lane (lr, lh) goes to 16-byte row 16(2(lr/16) + (lr/8)%2)
+      // + 8lh + 4(((lr/4)%2) ^ kq) + lr%4 of the tile's 1 KB block kq, so
+      // each store writes one whole block (layout in fa_bwd_ds.h).
+      const int prow = 16 * (2 * (lr >> 4) + ((lr >> 3) & 1)) + 8 * lh + (lr & 3);
+      const int g1 = (lr >> 2) & 1;
+      ds_store16(ds_c + 8 * (prow + 4 * g1), sB[0]);
+      ds_store16(ds_c + 512 + 8 * (prow + 4 * (g1 ^ 1)), sB[1]);
+    }
     // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS   (A operands by transpose reads)
     auto tr_ops = [&](int kq, int dt) {
       const int ro = kq * 16 * S::ROWB;
@@ -333,40 +358,54 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats) {
         }
       sched_pipeline<2 * (D / 32), 4, 2, 2>();
     }
+    return DS;
   };
 
   auto advance = [&](int& h_rel, int& it) {
     if (it-- == it0) {
       it = it1 - 1;
       ++h_rel;
+      if constexpr (DS) ds_c = ds_top + 1024 * h_rel * dsl.per_head();
+    } else if constexpr (DS) {
+      ds_c -= 1024 * dsl.count(it);
     }
   };
   int ih = 0, ii = it1 - 1;  // tile to issue next
   int ch = 0, ci = it1 - 1;  // tile to compute next
   // Iteration t: one barrier (Q/dO tile t landed, buffers of tile t-1 free),
   // then the DMA of tile t+1 and tile t's products.  The loop covers two
-  // tiles so that every buffer offset is an instruction immediate.
+  // tiles so that every buffer offset is an instruction immediate.  The
+  // wait before the barrier covers this wave's DMAs; the dS stores of the
+  // step before, issued after them, stay in flight (vector memory counts
+  // retire in issue order).
+  auto wait_tile = [&](bool stored) {
+    if (DS && stored)
+      __builtin_amdgcn_s_waitcnt(0x0F72);
+    else
+      wait_vmem();
+  };
+  bool stored = false;
   if (ntot > 0) {
     issue_q(ii, OFF_Q0, OFF_O0, OFF_ST0);
     advance_issue(ih, ii);
   }
   for (int t = 0; t < ntot; t += 2) {
-    wait_vmem();
+    wait_tile(stored);
     __syncthreads();
     if (t + 1 < ntot) {
       issue_q(ii, OFF_Q1, OFF_O1, OFF_ST1);
       advance_issue(ih, ii);
     }
-    step(ci, OFF_Q0, OFF_O0, OFF_ST0);
+    stored = step(ci, OFF_Q0, OFF_O0, OFF_ST0);
     advance(ch, ci);
     if (t + 1 >= ntot) break;
-    wait_vmem();
+    wait_tile(stored);
     __syncthreads();
     if (t + 2 < ntot) {
       issue_q(ii, OFF_Q0, OFF_O0, OFF_ST0);
       advance_issue(ih, ii);
     }
-    step(ci, OFF_Q1, OFF_O1, OFF_ST1);
+    stored = step(ci, OFF_Q1, OFF_O1, OFF_ST1);
     advance(ch, ci);
   }
   wait_vmem();

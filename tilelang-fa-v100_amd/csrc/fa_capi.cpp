@@ -157,16 +157,22 @@ size_t fa_bwd_workspace_bytes(const fa_bwd_args* a) {
   return fa::bwd_workspace_bytes(*a);
 }
 
+size_t fa_bwd_min_workspace_bytes(const fa_bwd_args* a) {
+  if (check_bwd(a) != FA_OK) return 0;
+  return fa::bwd_min_workspace_bytes(*a);
+}
+
 int fa_bwd(const fa_bwd_args* a, void* ws, size_t ws_bytes, void* stream) {
   const int st = check_bwd(a);
   if (st != FA_OK) return st;
   // seqlen_k == 0 with queries present still runs: dq is written as zero.
   if (a->batch == 0 || a->seqlen_q == 0) return ok();
-  const size_t need = fa::bwd_workspace_bytes(*a);
+  const size_t need = fa::bwd_min_workspace_bytes(*a);
   if (!ws || ws_bytes < need || !aligned16(ws))
     return fail(FA_E_WORKSPACE, "fa_bwd: workspace needs %zu bytes (16-byte aligned), got %zu",
                 need, ws ? ws_bytes : (size_t)0);
-  return hip_status(fa::launch_bwd(*a, ws, static_cast<hipStream_t>(stream)), "fa_bwd launch");
+  return hip_status(fa::launch_bwd(*a, ws, ws_bytes, static_cast<hipStream_t>(stream)),
+                    "fa_bwd launch");
 }
 
 // ------------------------------------------------------------------ paged

@@ -43,6 +43,11 @@ template <bool B>
 struct BoolC {
   static constexpr bool value = B;
 };
+// Compile-time integer tag.
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
 
 // Element-type traits.  `Half` is IEEE binary16, `BFloat16` is bfloat16.
 struct Half {

@@ -15,8 +15,13 @@ namespace fa {
 
 hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st);
 
+// bwd_workspace_bytes: the dS-store path's workspace where it applies
+// (head_dim 128, causal or full attention, dS tiles within
+// tiles::kBwdDsMaxBytes), else the row statistics only.
+// bwd_min_workspace_bytes: the row statistics (the recompute path).
 size_t bwd_workspace_bytes(const fa_bwd_args& a);
-hipError_t launch_bwd(const fa_bwd_args& a, void* ws, hipStream_t st);
+size_t bwd_min_workspace_bytes(const fa_bwd_args& a);
+hipError_t launch_bwd(const fa_bwd_args& a, void* ws, size_t ws_bytes, hipStream_t st);
 
 int paged_grid_slots(const fa_paged_args& a);
 hipError_t launch_paged_prefill(const fa_paged_args& a, hipStream_t st);

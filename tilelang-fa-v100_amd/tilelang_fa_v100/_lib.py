@@ -111,6 +111,7 @@ _PROTOTYPES = {
     "fa_last_error_message": (ctypes.c_char_p, []),
     "fa_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp]),
     "fa_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
+    "fa_bwd_min_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
     "fa_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
     "fa_paged_prefill": (ctypes.c_int, [ctypes.POINTER(PagedArgs), _vp]),
     "fa_paged_prefill_num_splits": (ctypes.c_int, [ctypes.POINTER(PagedArgs)]),
