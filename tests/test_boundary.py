@@ -130,12 +130,12 @@ def test_bwd_workspace_size_and_checks():
     rows = 4 * 2048 * 16
     stats = 2 * rows * 4 + 256
     # the row statistics (no dQ accumulator), whatever head_dim / `deterministic`;
-    # at head_dim 128 also the dS tiles (causal: 64 * 65 / 2 tiles per head)
+    # at head_dim 128 / 256 also the dS tiles (causal: 64 * 65 / 2 tiles per head)
     for hd in (64, 128, 256):
         for det in (0, 1):
             ad = bwd_args(head_dim=hd, deterministic=det)
             assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(ad)) == stats
-            ds = 2048 * 4 * 16 * (64 * 65 // 2) if hd == 128 else 0
+            ds = 2048 * 4 * 16 * (64 * 65 // 2) if hd in (128, 256) else 0
             assert lib.fa_bwd_workspace_bytes(ctypes.byref(ad)) == (stats + ds if ds else stats)
     # workspace missing / too small is rejected before any launch
     assert lib.fa_bwd(ctypes.byref(a), None, 0, None) == _lib.FA_E_WORKSPACE

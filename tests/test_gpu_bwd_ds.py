@@ -1,4 +1,4 @@
-"""GPU parity: the two dq paths of fa_bwd at head_dim 128.
+"""GPU parity: the two dq paths of fa_bwd at head_dim 128 and 256.
 
 With the workspace fa_bwd_workspace_bytes asks for, the dK / dV kernel stores
 its dS tiles and dq = scale * dS K is formed from them; with
@@ -22,21 +22,26 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 CASES = [
-    # (B, Sq, Sk, H, Hk, causal, dtype)
-    (1, 700, 700, 4, 4, True, torch.float16),
-    (1, 300, 500, 4, 2, True, torch.bfloat16),     # Sk > Sq, GQA
-    (1, 500, 300, 2, 2, True, torch.float16),      # Sq > Sk: rows that see no key
-    (2, 333, 333, 4, 4, False, torch.float16),     # full attention, ragged tiles
-    (1, 77, 1030, 2, 1, False, torch.bfloat16),    # MQA, one partial query tile
-    (1, 1, 300, 2, 2, True, torch.float16),        # one query row
-    (1, 40, 1, 2, 2, False, torch.float16),        # one key
-    (1, 2100, 2100, 2, 2, True, torch.float16),    # several 256-row query blocks
+    # (B, Sq, Sk, H, Hk, D, causal, dtype)
+    (1, 700, 700, 4, 4, 128, True, torch.float16),
+    (1, 300, 500, 4, 2, 128, True, torch.bfloat16),     # Sk > Sq, GQA
+    (1, 500, 300, 2, 2, 128, True, torch.float16),      # Sq > Sk: rows that see no key
+    (2, 333, 333, 4, 4, 128, False, torch.float16),     # full attention, ragged tiles
+    (1, 77, 1030, 2, 1, 128, False, torch.bfloat16),    # MQA, one partial query tile
+    (1, 1, 300, 2, 2, 128, True, torch.float16),        # one query row
+    (1, 40, 1, 2, 2, 128, False, torch.float16),        # one key
+    (1, 2100, 2100, 2, 2, 128, True, torch.float16),    # several 256-row query blocks
+    (1, 700, 700, 2, 2, 256, True, torch.float16),
+    (1, 300, 500, 4, 2, 256, True, torch.bfloat16),     # Sk > Sq, GQA
+    (1, 500, 300, 2, 2, 256, True, torch.float16),      # Sq > Sk
+    (2, 333, 200, 2, 1, 256, False, torch.float16),     # full attention, MQA
+    (1, 1, 90, 2, 2, 256, True, torch.float16),         # one query row
 ]
 
 
 def _ids(c):
-    B, Sq, Sk, H, Hk, causal, dt = c
-    return f"B{B}-{Sq}x{Sk}-H{H}/{Hk}-{'c' if causal else 'nc'}-{str(dt)[6:]}"
+    B, Sq, Sk, H, Hk, D, causal, dt = c
+    return f"B{B}-{Sq}x{Sk}-H{H}/{Hk}-D{D}-{'c' if causal else 'nc'}-{str(dt)[6:]}"
 
 
 def _bwd(q, k, v, out, lse, do, scale, causal, minimal):
@@ -45,7 +50,7 @@ def _bwd(q, k, v, out, lse, do, scale, causal, minimal):
     a = _dense.bwd_args(q, k, v, out, do, lse, dq, dk, dv, scale, causal, False)
     full = lib.fa_bwd_workspace_bytes(ctypes.byref(a))
     low = lib.fa_bwd_min_workspace_bytes(ctypes.byref(a))
-    assert low > 0 and full > low, "head_dim 128, causal / full: the dS path applies"
+    assert low > 0 and full > low, "head_dim 128 / 256, causal / full: the dS path applies"
     n = low if minimal else full
     ws = torch.full((n,), 0xFF, dtype=torch.uint8, device=DEV)
     _lib.check(_lib.call_on(q.device, lambda st: lib.fa_bwd(ctypes.byref(a), ws.data_ptr(), n,
@@ -56,8 +61,7 @@ def _bwd(q, k, v, out, lse, do, scale, causal, minimal):
 
 @pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
 def test_dq_paths_match_oracle_and_each_other(case):
-    B, Sq, Sk, H, Hk, causal, dt = case
-    D = 128
+    B, Sq, Sk, H, Hk, D, causal, dt = case
     g = torch.Generator().manual_seed(41)
     q, do = randn(g, B, Sq, H, D, dtype=dt), None
     k, v = randn(g, B, Sk, Hk, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt)

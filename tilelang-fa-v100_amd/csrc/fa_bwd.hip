@@ -25,7 +25,7 @@
 //                       tiles of every query head that shares the KV head
 //                       (GQA).  K and V of the wave stay in registers.
 //   bwd_main_mfma_kernel  head_dim 128 / 256 dK / dV (fa_bwd_mfma.h).
-// At head_dim 128 with causal or full attention and a workspace of
+// At head_dim 128 / 256 with causal or full attention and a workspace of
 // bwd_workspace_bytes, the order is instead bwd_stats_kernel (the row
 // statistics), bwd_main_mfma_kernel<..., DS = true> (dK / dV, storing its dS
 // tiles) and bwd_dq_ds_kernel (dQ = scale · dS K from them), fa_bwd_ds.h.
@@ -288,10 +288,12 @@ static size_t stats_bytes(const fa_bwd_args& a) {
 static size_t ds_offset(const fa_bwd_args& a) { return (stats_bytes(a) + 255) & ~(size_t)255; }
 
 // Bytes of dS tiles for the dS-store path, or 0 where it does not apply:
-// head_dim 128, causal or full attention, at most tiles::kBwdDsMaxBytes.
+// head_dim 128 / 256, causal or full attention, at most tiles::kBwdDsMaxBytes.
 static size_t ds_bytes(const fa_bwd_args& a) {
   const int mode = mask_mode(a);
-  if (a.head_dim != 128 || mode == kMaskBand || a.seqlen_q <= 0 || a.seqlen_k <= 0) return 0;
+  if ((a.head_dim != 128 && a.head_dim != 256) || mode == kMaskBand || a.seqlen_q <= 0 ||
+      a.seqlen_k <= 0)
+    return 0;
   const DsTiles L = mode == kMaskCausal ? ds_tiles<kMaskCausal>(a.seqlen_q, a.seqlen_k)
                                         : ds_tiles<kMaskNone>(a.seqlen_q, a.seqlen_k);
   const size_t bytes = 2048 * (size_t)a.batch * a.num_heads * (size_t)L.per_head();
@@ -306,7 +308,7 @@ size_t bwd_workspace_bytes(const fa_bwd_args& a) {
 }
 
 // Key-stationary dK / dV kernel for one mask mode; with ds, also stores the
-// dS tiles (head_dim 128, causal or full attention).
+// dS tiles (head_dim 128 / 256, causal or full attention).
 template <class T, int D>
 static void launch_bwd_main(const fa_bwd_args& a, int mode, const float* stats, uint16_t* ds,
                             hipStream_t st) {
@@ -315,7 +317,7 @@ static void launch_bwd_main(const fa_bwd_args& a, int mode, const float* stats, 
     const int kvtiles = (a.seqlen_k + S::BKV - 1) / S::BKV;
     const dim3 grid((unsigned)kvtiles * a.num_heads_k * a.batch), block(64 * S::NW);
     if (kvtiles == 0) return;  // no keys: dK / dV are empty
-    if constexpr (D == 128) {
+    {
       if (ds) {
         if (mode == kMaskCausal)
           hipLaunchKernelGGL((bwd_main_mfma_kernel<T, D, kMaskCausal, true>), grid, block, 0, st,
@@ -363,26 +365,26 @@ static void launch_bwd_dq(const fa_bwd_args& a, int mode, float* stats, hipStrea
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, kMaskNone>), grid, block, 0, st, a, stats);
 }
 
-// dS-store path (head_dim 128): row statistics, dK / dV storing dS, then
-// dQ = scale · dS K.
-template <class T>
+// dS-store path (head_dim 128 / 256): row statistics, dK / dV storing dS,
+// then dQ = scale · dS K.
+template <class T, int D>
 static hipError_t launch_bwd_ds(const fa_bwd_args& a, int mode, void* ws, hipStream_t st) {
   float* stats = static_cast<float*>(ws);
   uint16_t* ds = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + ds_offset(a));
   const int64_t waves = (int64_t)a.batch * a.num_heads * ((a.seqlen_q + 31) / 32);
-  hipLaunchKernelGGL((bwd_stats_kernel<T, 128>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+  hipLaunchKernelGGL((bwd_stats_kernel<T, D>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
                      st, a, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch_bwd_main<T, 128>(a, mode, stats, ds, st);
+  launch_bwd_main<T, D>(a, mode, stats, ds, st);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int nqb = ((a.seqlen_q + 31) / 32 + 7) / 8;
   const dim3 grid((unsigned)nqb * a.num_heads * a.batch), block(512);
   if (mode == kMaskCausal)
-    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, kMaskCausal>), grid, block, 0, st, a, ds);
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D, kMaskCausal>), grid, block, 0, st, a, ds);
   else
-    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, kMaskNone>), grid, block, 0, st, a, ds);
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D, kMaskNone>), grid, block, 0, st, a, ds);
   return hipGetLastError();
 }
 
@@ -393,8 +395,9 @@ static hipError_t launch_bwd_ds(const fa_bwd_args& a, int mode, void* ws, hipStr
 template <class T, int D>
 static hipError_t launch_bwd_d(const fa_bwd_args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const int mode = mask_mode(a);
-  if (D == 128 && ds_bytes(a) && ws_bytes >= bwd_workspace_bytes(a))
-    return launch_bwd_ds<T>(a, mode, ws, st);
+  if constexpr (D >= 128) {
+    if (ds_bytes(a) && ws_bytes >= bwd_workspace_bytes(a)) return launch_bwd_ds<T, D>(a, mode, ws, st);
+  }
   float* stats = static_cast<float*>(ws);  // [B*H][2][Sq]
   launch_bwd_dq<T, D>(a, mode, stats, st);
   hipError_t e = hipGetLastError();

@@ -1,5 +1,5 @@
-// dQ of the dense attention backward from stored dS tiles (head_dim 128,
-// causal or full attention).
+// dQ of the dense attention backward from stored dS tiles (head_dim 128 and
+// 256, causal or full attention).
 //
 // The key-stationary dK / dV kernel (fa_bwd_mfma.h) forms dS = P (dP − rowdot)
 // for every (query tile, key block) pair it visits.  With its DS variant it
@@ -117,11 +117,11 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(fa_bwd_args a, float* st
   }
 }
 
-// dQ = scale · Σ_kb dS(qt, kb) K(kb) for head_dim 128.  Workgroup: 8 waves,
-// wave w owns query tile qt = 8 qb + w of one query head; steps run over
-// 32-key blocks.  Per step, wave w copies rows 4w..4w+3 of the K tile and
-// its own 2 KB dS tile HBM -> LDS (buffer DMA: K rows past Sk and dS tiles
-// past the wave's count read as zero), NBUF stages, NBUF - 1 in flight.
+// dQ = scale · Σ_kb dS(qt, kb) K(kb) for head_dim 128 / 256.  Workgroup: 8
+// waves, wave w owns query tile qt = 8 qb + w of one query head; steps run
+// over 32-key blocks.  Per step, wave w copies rows 4w..4w+3 of the K tile
+// and its own 2 KB dS tile HBM -> LDS (buffer DMA: K rows past Sk and dS
+// tiles past the wave's count read as zero), NBUF stages, NBUF - 1 in flight.
 // Products (the layout of bwd_dq_kernel's dQᵀ += Kᵀ dSᵀ):
 //   A = Kᵀ (d x key) by ds_read_b64_tr_b16 of the row-major K tile (16-byte
 //       chunk swizzle of fa_fwd_d128.h), B = dSᵀ (key x query) by
@@ -130,16 +130,33 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(fa_bwd_args a, float* st
 // bytes read by lane 16g + 4j + i/4; both operands are read so that lane l
 // gets keys 16kc + 8(l/32) + 4r + j (read r = 0, 1) of column l%32 (d for A,
 // query for B).
-template <class T, int MODE>
-__global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const uint16_t* ds) {
-  constexpr int D = 128, NW = 8, ROWB = 256, NBUF = 3;
-  constexpr int KTB = 32 * ROWB;     // K tile: 32 keys x 256 B
-  constexpr int OFF_S = NBUF * KTB;  // dS stages after the K stages
-  constexpr int SSB = NW * 2048;     // dS stage: one tile per wave
-  // Two workgroups per CU (72 KB of LDS and at most 128 registers each):
-  // T1 435 -> 420 us against one workgroup with six stages.
-  static_assert(2 * (OFF_S + NBUF * SSB) <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) char smem[OFF_S + NBUF * SSB];
+template <int D>
+struct DqDsShape {
+  static constexpr int NW = 8;
+  static constexpr int ROWB = 2 * D;             // bytes per K row
+  static constexpr int RPB = 1024 / ROWB;        // K rows per 1 KB DMA block
+  static constexpr int CPR = D / 8;              // 16-byte chunks per row
+  static constexpr int KBPW = 32 / RPB / NW;     // K blocks per wave and step
+  // head_dim 128: two workgroups per CU (72 KB of LDS, at most 128 registers
+  // each; T1 435 -> 420 us against one workgroup with six stages).  head_dim
+  // 256: one workgroup (dQ of 32 rows x 256 d takes 128 registers).
+  static constexpr int NBUF = D == 128 ? 3 : 4;
+  static constexpr int WPE = D == 128 ? 4 : 2;   // waves per SIMD
+  static constexpr int KTB = 32 * ROWB;          // K tile: 32 keys
+  static constexpr int OFF_S = NBUF * KTB;       // dS stages after the K stages
+  static constexpr int SSB = NW * 2048;          // dS stage: one tile per wave
+  static constexpr int LDS = OFF_S + NBUF * SSB;
+  static_assert((D == 128 || D == 256) && KBPW * RPB * NW == 32, "shape");
+  static_assert(LDS * (WPE / 2) <= 160 * 1024, "LDS");
+};
+
+template <class T, int D, int MODE>
+__global__ __launch_bounds__(512, DqDsShape<D>::WPE) void bwd_dq_ds_kernel(fa_bwd_args a,
+                                                                           const uint16_t* ds) {
+  using Sh = DqDsShape<D>;
+  constexpr int NW = Sh::NW, ROWB = Sh::ROWB, NBUF = Sh::NBUF, KTB = Sh::KTB, KBPW = Sh::KBPW;
+  constexpr int OFF_S = Sh::OFF_S, SSB = Sh::SSB;
+  __shared__ __attribute__((aligned(16))) char smem[Sh::LDS];
 
   const int Sq = a.seqlen_q, Sk = a.seqlen_k, H = a.num_heads;
   const DsTiles L = ds_tiles<MODE>(Sq, Sk);
@@ -155,13 +172,18 @@ __global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const 
   const int cnt = qt < L.nq ? L.count(qt) : 0;
   const int nsteps = L.count(min(NW * qb + NW - 1, L.nq - 1));
 
-  // K rows 32s + 4w + lane/16, stored chunk lane%16 (logical chunk
-  // (lane%16) ^ swz(row)); the lane's byte offset from the wave's first row
-  // is fixed.
+  // K rows 32s + 4w + rr, rr = RPB i + lane / CPR in block i, stored chunk
+  // lane % CPR (logical chunk (lane % CPR) ^ swz(row), the swizzle acting on
+  // the low four chunk bits); the lane's byte offset from the wave's first
+  // row is fixed.
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
-  const int kr = lane >> 4;
-  const uint32_t k_loff =
-      2u * (kr * (uint32_t)a.k_stride[1] + 8 * ((lane & 15) ^ swz_chunk(4 * wave + kr)));
+  uint32_t k_loff[KBPW];
+#pragma unroll
+  for (int i = 0; i < KBPW; ++i) {
+    const int rr = Sh::RPB * i + lane / Sh::CPR;
+    k_loff[i] = 2u * (rr * (uint32_t)a.k_stride[1] +
+                      8 * ((lane % Sh::CPR) ^ swz_chunk(4 * wave + rr)));
+  }
   const uint16_t* ds_w =
       ds + 1024 * ((int64_t)bh * L.per_head() + L.prefix(min(qt, L.nq)));
   const u32x4 rs = rsrc_words(ds_w, (uint32_t)cnt * 2048u);
@@ -170,7 +192,9 @@ __global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const 
     const int nvalid = max(min(4, Sk - nb), 0);
     const u32x4 rk = rsrc_words(kg + (int64_t)nb * a.k_stride[1],
                                 span_bytes(nvalid, a.k_stride[1], D));
-    buffer_lds16_opaque(rk, k_loff, smem + stage * KTB + wave * 1024);
+#pragma unroll
+    for (int i = 0; i < KBPW; ++i)
+      buffer_lds16_opaque(rk, k_loff[i], smem + stage * KTB + (KBPW * wave + i) * 1024);
     const uint32_t so = (uint32_t)s * 2048u + 16u * lane;
     char* sd = smem + OFF_S + stage * SSB + wave * 2048;
     buffer_lds16_stream(rs, so, sd);
@@ -183,12 +207,12 @@ __global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const 
   // (+16 per key chunk), half lane%2 and chunk kq = (lane/16)%2 of the
   // writer, i.e. row 16(lane/32) + 8(lane%2) + 4(r ^ kq) + (lane%16)/4 of
   // block kq (+32 rows = 512 bytes per key chunk), 8-byte half (lane%4)/2.
-  int aoff[2][4], boff[2];
+  int aoff[2][D / 32], boff[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int row = 8 * lh + 4 * r + ((lane & 15) >> 2);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < D / 32; ++dt) {
       const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
       aoff[r][dt] = row * ROWB + 16 * (chunk ^ swz_chunk(row)) + 8 * (lane & 1);
     }
@@ -198,9 +222,9 @@ __global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const 
               8 * ((lane & 3) >> 1);
   }
 
-  f32x16 acc[4];
+  f32x16 acc[D / 32];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
@@ -213,27 +237,28 @@ __global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const 
       const u32x2 b1 = lds_read_tr(st + boff[1] + 512 * kc);
       const u32x4 bs = {b0[0], b0[1], b1[0], b1[1]};
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const u32x2 a0 = lds_read_tr(kt + aoff[0][dt] + 4096 * kc);
-        const u32x2 a1 = lds_read_tr(kt + aoff[1][dt] + 4096 * kc);
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const u32x2 a0 = lds_read_tr(kt + aoff[0][dt] + 16 * ROWB * kc);
+        const u32x2 a1 = lds_read_tr(kt + aoff[1][dt] + 16 * ROWB * kc);
         acc[dt] = T::mma32(u32x4{a0[0], a0[1], a1[0], a1[1]}, bs, acc[dt]);
       }
     }
   };
 
-  // Step s: wait for this wave's DMAs of stage s (3 per stage; the
+  // Step s: wait for this wave's DMAs of stage s (KBPW + 2 per stage; the
   // min(NBUF - 2, nsteps - 1 - s) stages after it stay in flight), barrier
   // (every wave's part of the K tile landed; the stage of step s - 1 is
   // free), refill that stage with step s + NBUF - 1.
-  static_assert(NBUF >= 3 && NBUF <= 6, "waits below");
+  constexpr int PER_STAGE = KBPW + 2;
+  static_assert((NBUF - 2) * PER_STAGE <= 8, "waits below");
   for (int s = 0; s < NBUF - 1 && s < nsteps; ++s) issue(s, s);
   int stage = 0;
   for (int s = 0; s < nsteps; ++s) {
-    switch (min(NBUF - 2, nsteps - 1 - s)) {
-      case 4: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-      case 3: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-      case 2: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-      case 1: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    switch (min(NBUF - 2, nsteps - 1 - s) * PER_STAGE) {
+      case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
       default: wait_vmem(); break;
     }
     __syncthreads();
@@ -250,7 +275,7 @@ __global__ __launch_bounds__(512, 4) void bwd_dq_ds_kernel(fa_bwd_args a, const 
   uint16_t* dqp = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] +
                   (int64_t)row * a.dq_stride[1] + h * a.dq_stride[2];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       u32x2 w;

@@ -50,7 +50,7 @@ struct TrOps {
 
 // MODE (MaskMode): full attention, causal, or a window band from the arguments.
 // DS: also store every computed 32 x 32 dS block to `ds` (tile layout of
-// fa_bwd_ds.h; head_dim 128, causal or full attention) for bwd_dq_ds_kernel.
+// fa_bwd_ds.h; causal or full attention) for bwd_dq_ds_kernel.
 template <class T, int D_, int MODE, bool DS = false>
 __global__ __launch_bounds__((64 * BwdShapeMfma<D_>::NW), (BwdShapeMfma<D_>::WPE))
 void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
@@ -193,7 +193,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
   const float* s_i = s_top;
   // DS: the dS tile of the tile `step` computes next (same sweep order as
   // the issue side), stepped back by count(it) tiles per query tile.
-  static_assert(!DS || (D == 128 && MODE != kMaskBand), "dS tiles: head_dim 128, causal or full");
+  static_assert(!DS || MODE != kMaskBand, "dS tiles: causal or full attention");
   DsTiles dsl{1, 1, 1};
   uint16_t* ds_top = nullptr;
   if constexpr (DS) {

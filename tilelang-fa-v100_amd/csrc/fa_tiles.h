@@ -71,10 +71,10 @@ constexpr int kBwdQueryRows = 32;
 // The atomics are performed beyond the XCD's L2 on this part, ~64 address
 // cycles per instruction, a floor of ~1.17 ms for T1's backward.
 
-// ---- backward: dQ from stored dS tiles (fa_bwd_ds.h), head_dim 128, causal
-// or full attention, while the tiles (2 bytes per visible (query, key) pair,
-// 2.15 GB at T1) stay within this many bytes; larger problems recompute S and
-// dP in bwd_dq_kernel.
+// ---- backward: dQ from stored dS tiles (fa_bwd_ds.h), head_dim 128 / 256,
+// causal or full attention, while the tiles (2 bytes per visible (query, key)
+// pair, 2.15 GB at T1) stay within this many bytes; larger problems recompute
+// S and dP in bwd_dq_kernel.
 constexpr size_t kBwdDsMaxBytes = size_t(4) << 30;
 
 // ---- backward main kernel, head_dim 64 (fa_bwd.hip)
