@@ -9,9 +9,9 @@ tilelang_flash_attn_func forward + autograd backward over resident inputs.
 value = algorithmic FLOPs per step / step time (FLOPs over unmasked pairs
 only: fwd 4*D*H*pairs, bwd 2.5x fwd).
 
-`roofline` covers the dominant launch of that step, the fa_bwd call (its
-dQ (with the row statistics) and dK / dV kernels), timed with HIP events on the stream it is
-launched on; its `traffic` (HBM bytes per launch) comes from the counter
+`roofline` covers the dominant launch of that step, the fa_bwd call (row
+statistics, dK / dV storing the dS tiles, dQ from them), timed with HIP events
+on the stream it is launched on; its `traffic` (HBM bytes per launch) comes from the counter
 runs summarised in profiles/fa_bwd_c2_traffic.md.  `extra` reports the other
 BASELINE configs and the north-star points (T1: S=8192 fwd+bwd, T2: decode
 at 32k context) with their own roofline fractions; paged/decode reps flush
@@ -297,7 +297,8 @@ def headline(fa, steps, warmup, dev):
     roofline = {"bound": "mfma", "achieved": round(bwd_tf, 1), "peak": PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(bwd_tf / PEAK_TFLOPS, 4),
                 "traffic": profiled_traffic("fa_bwd_c2"),
-                "kernel": "fa_bwd (bwd_dq dQ + row statistics, bwd_main_mfma dK/dV)",
+                "kernel": "fa_bwd (bwd_stats row statistics, bwd_main_mfma dK/dV + dS tiles, "
+                          "bwd_dq_ds dQ)",
                 "launch_ms": round(bwd_ms, 4), "algorithmic_gflop": round(2.5 * f_fwd / 1e9, 2)}
     parts = dict([flop_entry("C2_fwd", f_fwd, fwd_ms, fwd_api),
                   flop_entry("C2_bwd", 2.5 * f_fwd, bwd_ms, bwd_api)])
