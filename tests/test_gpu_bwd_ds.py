@@ -31,6 +31,7 @@ CASES = [
     (1, 1, 300, 2, 2, 128, True, torch.float16),        # one query row
     (1, 40, 1, 2, 2, 128, False, torch.float16),        # one key
     (1, 2100, 2100, 2, 2, 128, True, torch.float16),    # several 256-row query blocks
+    (2, 2080, 2080, 32, 8, 128, True, torch.float16),   # GQA 4:1, 576 dQ workgroups
     (1, 700, 700, 2, 2, 256, True, torch.float16),
     (1, 300, 500, 4, 2, 256, True, torch.bfloat16),     # Sk > Sq, GQA
     (1, 500, 300, 2, 2, 256, True, torch.float16),      # Sq > Sk
