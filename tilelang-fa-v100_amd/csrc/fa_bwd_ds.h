@@ -96,6 +96,8 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(fa_bwd_args a, float* st
   const int row = (gw % tiles) * 32 + lr;
   const int h = bh % H, b = bh / H;
   const int64_t r = min(row, Sq - 1);
+  // Issued first: its latency overlaps the row loads below.
+  const float l = a.lse[(int64_t)bh * Sq + r];
   const uint16_t* dp = static_cast<const uint16_t*>(a.dout) + b * a.do_stride[0] +
                        h * a.do_stride[2] + r * a.do_stride[1];
   const uint16_t* op = static_cast<const uint16_t*>(a.out) + b * a.o_stride[0] +
@@ -110,7 +112,6 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(fa_bwd_args a, float* st
   }
   const float full = half_sum(part);
   if (row < Sq && lh == 0) {
-    const float l = a.lse[(int64_t)bh * Sq + row];
     float* st = stats + 2 * (int64_t)bh * Sq;
     st[row] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
     st[Sq + row] = full;
@@ -137,11 +138,11 @@ struct DqDsShape {
   static constexpr int RPB = 1024 / ROWB;        // K rows per 1 KB DMA block
   static constexpr int CPR = D / 8;              // 16-byte chunks per row
   static constexpr int KBPW = 32 / RPB / NW;     // K blocks per wave and step
-  // head_dim 128: two workgroups per CU (72 KB of LDS, at most 128 registers
-  // each; T1 435 -> 420 us against one workgroup with six stages).  head_dim
-  // 256: one workgroup (dQ of 32 rows x 256 d takes 128 registers).
-  static constexpr int NBUF = D == 128 ? 3 : 4;
-  static constexpr int WPE = D == 128 ? 4 : 2;   // waves per SIMD
+  // One workgroup per CU, four stages (three in flight).  head_dim 128, same
+  // box, dQ kernel: C2 65.8 us against 77.4 (two workgroups per CU with three
+  // stages each) and 68.3 (one with six); T1 within noise of both (418-435 us).
+  static constexpr int NBUF = 4;
+  static constexpr int WPE = 2;                  // waves per SIMD
   static constexpr int KTB = 32 * ROWB;          // K tile: 32 keys
   static constexpr int OFF_S = NBUF * KTB;       // dS stages after the K stages
   static constexpr int SSB = NW * 2048;          // dS stage: one tile per wave
@@ -250,11 +251,13 @@ __global__ __launch_bounds__(512, DqDsShape<D>::WPE) void bwd_dq_ds_kernel(fa_bw
   // (every wave's part of the K tile landed; the stage of step s - 1 is
   // free), refill that stage with step s + NBUF - 1.
   constexpr int PER_STAGE = KBPW + 2;
-  static_assert((NBUF - 2) * PER_STAGE <= 8, "waits below");
+  static_assert((NBUF - 2) * PER_STAGE <= 12, "waits below");
   for (int s = 0; s < NBUF - 1 && s < nsteps; ++s) issue(s, s);
   int stage = 0;
   for (int s = 0; s < nsteps; ++s) {
     switch (min(NBUF - 2, nsteps - 1 - s) * PER_STAGE) {
+      case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+      case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
       case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
       case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
       case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
