@@ -379,8 +379,9 @@ static hipError_t launch_bwd_ds(const fa_bwd_args& a, int mode, void* ws, hipStr
   launch_bwd_main<T, D>(a, mode, stats, ds, st);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int nqb = ((a.seqlen_q + 31) / 32 + 7) / 8;
-  const dim3 grid((unsigned)nqb * a.num_heads * a.batch), block(512);
+  constexpr int NW = DqDsShape<D>::NW;
+  const int nqb = ((a.seqlen_q + 31) / 32 + NW - 1) / NW;
+  const dim3 grid((unsigned)nqb * a.num_heads * a.batch), block(64 * NW);
   if (mode == kMaskCausal)
     hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D, kMaskCausal>), grid, block, 0, st, a, ds);
   else

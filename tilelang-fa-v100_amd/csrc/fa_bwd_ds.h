@@ -133,11 +133,12 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(fa_bwd_args a, float* st
 // query for B).
 template <int D>
 struct DqDsShape {
-  static constexpr int NW = 8;
+  static constexpr int NW = 8;                   // (4: C2 71.4 against 68.2 us)
+  static constexpr int RW = 32 / NW;             // K rows each wave copies per step
   static constexpr int ROWB = 2 * D;             // bytes per K row
   static constexpr int RPB = 1024 / ROWB;        // K rows per 1 KB DMA block
   static constexpr int CPR = D / 8;              // 16-byte chunks per row
-  static constexpr int KBPW = 32 / RPB / NW;     // K blocks per wave and step
+  static constexpr int KBPW = RW / RPB;          // K blocks per wave and step
   // One workgroup per CU, four stages (three in flight).  head_dim 128, same
   // box, dQ kernel: C2 65.8 us against 77.4 (two workgroups per CU with three
   // stages each) and 68.3 (one with six); T1 within noise of both (418-435 us).
@@ -152,8 +153,8 @@ struct DqDsShape {
 };
 
 template <class T, int D, int MODE>
-__global__ __launch_bounds__(512, DqDsShape<D>::WPE) void bwd_dq_ds_kernel(fa_bwd_args a,
-                                                                           const uint16_t* ds) {
+__global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_dq_ds_kernel(
+    fa_bwd_args a, const uint16_t* ds) {
   using Sh = DqDsShape<D>;
   constexpr int NW = Sh::NW, ROWB = Sh::ROWB, NBUF = Sh::NBUF, KTB = Sh::KTB, KBPW = Sh::KBPW;
   constexpr int OFF_S = Sh::OFF_S, SSB = Sh::SSB;
@@ -183,14 +184,14 @@ __global__ __launch_bounds__(512, DqDsShape<D>::WPE) void bwd_dq_ds_kernel(fa_bw
   for (int i = 0; i < KBPW; ++i) {
     const int rr = Sh::RPB * i + lane / Sh::CPR;
     k_loff[i] = 2u * (rr * (uint32_t)a.k_stride[1] +
-                      8 * ((lane % Sh::CPR) ^ swz_chunk(4 * wave + rr)));
+                      8 * ((lane % Sh::CPR) ^ swz_chunk(Sh::RW * wave + rr)));
   }
   const uint16_t* ds_w =
       ds + 1024 * ((int64_t)bh * L.per_head() + L.prefix(min(qt, L.nq)));
   const u32x4 rs = rsrc_words(ds_w, (uint32_t)cnt * 2048u);
   auto issue = [&](int s, int stage) {
-    const int nb = 32 * s + 4 * wave;
-    const int nvalid = max(min(4, Sk - nb), 0);
+    const int nb = 32 * s + Sh::RW * wave;
+    const int nvalid = max(min(Sh::RW, Sk - nb), 0);
     const u32x4 rk = rsrc_words(kg + (int64_t)nb * a.k_stride[1],
                                 span_bytes(nvalid, a.k_stride[1], D));
 #pragma unroll
