@@ -39,7 +39,8 @@
 extern "C" {
 #endif
 
-#define FA355_ABI_VERSION 2
+/* 3: fa_bwd_min_workspace_bytes; fa_bwd_workspace_bytes includes the dS tiles. */
+#define FA355_ABI_VERSION 3
 
 typedef enum fa_status {
   FA_OK = 0,

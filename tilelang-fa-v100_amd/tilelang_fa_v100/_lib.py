@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 
 LIB_NAME = "libfa355.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FA_OK = 0
 FA_E_INVALID = -1
