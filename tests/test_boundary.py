@@ -143,6 +143,8 @@ def test_bwd_workspace_size_and_checks():
     assert lib.fa_bwd(ctypes.byref(bwd_args(head_dim=96)), 0x4000, 1 << 40, None) == \
         _lib.FA_E_UNSUPPORTED
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(bwd_args(lse=None))) == 0
+    assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(bwd_args(lse=None))) == 0
+    assert lib.fa_bwd_min_workspace_bytes(None) == 0
     # (batch, head) pairs beyond the grid-y limit are refused, not truncated
     big = bwd_args(batch=4096, num_heads=16, num_heads_k=16, seqlen_q=16, seqlen_k=16)
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(big)) == 0
