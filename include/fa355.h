@@ -98,7 +98,7 @@ int fa_fwd(const fa_fwd_args* args, void* stream);
 
 /* Backward: LSE-recompute FlashAttention-2 gradient.  dq/dk/dv use the same
  * layout rules as q/k/v.  The workspace holds the per-row statistics (LSE and
- * dot(O, dO)) and, at head_dim 128 with causal or full attention, the 16-bit
+ * dot(O, dO)) and, at head_dim 128 or 256 with causal or full attention, the 16-bit
  * dS tiles from which dq is formed (2 bytes per (query, key) pair the mask
  * lets through, up to 4 GiB); fa_bwd_workspace_bytes gives that size.  A
  * workspace of at least fa_bwd_min_workspace_bytes (the statistics only)
