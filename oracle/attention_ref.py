@@ -94,13 +94,18 @@ def dense_attention(q, k, v, scale=None, causal=False, dtype=torch.float32, wind
 
 
 def dense_attention_backward(q, k, v, dout, scale=None, causal=False, dtype=torch.float32,
-                             window=(-1, -1)):
+                             window=(-1, -1), round_dtype=None):
     """Gradients of dense_attention w.r.t. q, k, v by the FlashAttention-2
     formulas the reference kernels implement:
       P = exp(scale*S - lse), rowdot = sum_d O*dO   (_kernels_backward.py:203)
-      dP = dO V^T, dS = P * (dP - rowdot)          (:55, :72-74, :157-163)
-      dV = P^T dO, dK = scale * dS^T Q, dQ = scale * dS K   (:80, :165-170)
+      dP = dO V^T, dS = P * (dP - rowdot) * scale  (:55, :72-74, :157-163)
+      dV = P^T dO, dK = dS^T Q, dQ = dS K           (:80, :165-170)
     GQA: dK / dV of a KV head sum over its query-head group.
+    round_dtype (e.g. torch.float16): also restate the reference's roundings
+    to 16 bits - rowdot from the 16-bit forward output (:203 reads out_),
+    P rounded before dV (:162-166) and scale*dS rounded before dK and dQ
+    (:74-80, :167-170) - with the products still accumulated in `dtype`.
+    None (default): no rounding, the exact gradient in `dtype`.
     Returns dq, dk, dv in `dtype`.
     """
     B, Sq, H, D = q.shape
@@ -121,12 +126,17 @@ def dense_attention_backward(q, k, v, dout, scale=None, causal=False, dtype=torc
         lse = torch.where(torch.isneginf(lse), torch.full_like(lse, float("inf")), lse)
         p = torch.exp(s - lse)                                    # [H, Sq, Sk]
         o = torch.einsum("hqk,khd->qhd", p, ve[b])
+        if round_dtype is not None:
+            o = o.to(round_dtype).to(dtype)
         rowdot = (o * dof[b]).sum(-1).transpose(0, 1).unsqueeze(-1)   # [H, Sq, 1]
         dp = torch.einsum("qhd,khd->hqk", dof[b], ve[b])
-        ds = p * (dp - rowdot)
+        ds = p * (dp - rowdot) * scale
+        if round_dtype is not None:
+            p = p.to(round_dtype).to(dtype)
+            ds = ds.to(round_dtype).to(dtype)
         dve[b] = torch.einsum("hqk,qhd->khd", p, dof[b])
-        dke[b] = torch.einsum("hqk,qhd->khd", ds, qf[b]) * scale
-        dq[b] = torch.einsum("hqk,khd->qhd", ds, ke[b]) * scale
+        dke[b] = torch.einsum("hqk,qhd->khd", ds, qf[b])
+        dq[b] = torch.einsum("hqk,khd->qhd", ds, ke[b])
     dk = dke.view(B, Sk, Hk, g, D).sum(3)
     dv = dve.view(B, Sk, Hk, g, D).sum(3)
     return dq, dk, dv

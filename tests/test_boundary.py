@@ -145,10 +145,20 @@ def test_bwd_workspace_size_and_checks():
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(bwd_args(lse=None))) == 0
     assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(bwd_args(lse=None))) == 0
     assert lib.fa_bwd_min_workspace_bytes(None) == 0
-    # (batch, head) pairs beyond the grid-y limit are refused, not truncated
+    # Every grid is one-dimensional: 65536 (batch, head) pairs are accepted,
+    # as fa_fwd accepts them, so a training step cannot pass its forward and
+    # fail in its backward (tests/test_gpu_dense.py runs such a problem) ...
     big = bwd_args(batch=4096, num_heads=16, num_heads_k=16, seqlen_q=16, seqlen_k=16)
-    assert lib.fa_bwd_workspace_bytes(ctypes.byref(big)) == 0
-    assert b"65535" in lib.fa_last_error_message()
+    for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv"):
+        getattr(big, f"{n}_stride")[:] = (16 * 16 * 128, 16 * 128, 128)
+    stats = 2 * 4096 * 16 * 16 * 4 + 256
+    assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(big)) == stats
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(big)) == \
+        (stats + 255) // 256 * 256 + 2048 * 4096 * 16
+    # ... while grids beyond 32-bit workgroup counts are refused, not truncated
+    huge = bwd_args(batch=1 << 20, num_heads=4096, num_heads_k=4096, seqlen_q=1, seqlen_k=1)
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(huge)) == 0
+    assert b"too large" in lib.fa_last_error_message()
 
 
 def _ds_tiles_brute(sq, sk, causal):
@@ -199,6 +209,21 @@ def test_bwd_ds_workspace_cap():
         getattr(a, f"{n}_stride")[:] = (s * 3 * 128, 3 * 128, 128)
     stats = 2 * 3 * s * 4 + 256
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == stats + 2048 * 3 * per_head
+    # Exactly 4 GiB (one query tile reaching 2^21 key blocks): a wave's dS
+    # reads use one buffer resource of count * 2 KB bytes, a 32-bit size that
+    # would wrap to zero, so the cap is strict.
+    for causal in (0, 1):
+        a = bwd_args(batch=1, num_heads=1, num_heads_k=1, seqlen_q=32, seqlen_k=1 << 26,
+                     causal=causal)
+        for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv"):
+            getattr(a, f"{n}_stride")[:] = (a.seqlen_q * 128 if n in ("q", "o", "do", "dq")
+                                            else (1 << 26) * 128, 128, 128)
+        stats = 2 * 32 * 4 + 256
+        assert lib.fa_bwd_min_workspace_bytes(ctypes.byref(a)) == stats
+        assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == stats
+        a.seqlen_k = (1 << 26) - 32  # one key block fewer: under the cap
+        assert lib.fa_bwd_workspace_bytes(ctypes.byref(a)) == \
+            (stats + 255) // 256 * 256 + 2048 * ((1 << 21) - 1)
 
 
 def paged_args(**over):

@@ -84,3 +84,33 @@ def test_dq_paths_match_oracle_and_each_other(case):
             assert_close(got, r[i], what=name)
             if r[i].abs().max() > 1e-4:
                 assert rel_l2(got, r[i]) < 1e-2, name
+
+
+def test_public_backward_honours_workspace_limit():
+    """tilelang_flash_attn_func's backward takes the dS path by default and
+    the recompute path (the reference's memory footprint) when the workspace
+    limit is below the dS workspace: its gradients then equal fa_bwd's with
+    the minimal workspace bit for bit, and both match the oracle."""
+    import tilelang_fa_v100 as fa
+
+    B, S, H, D = 1, 900, 4, 128
+    g = torch.Generator().manual_seed(43)
+    q, k, v, do = (randn(g, B, S, H, D) for _ in range(4))
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    scale = D ** -0.5
+    out, lse = _dense.forward(qd, kd, vd, scale, True)
+    ds_path = _bwd(qd, kd, vd, out, lse, dod, scale, True, minimal=False)
+    rc_path = _bwd(qd, kd, vd, out, lse, dod, scale, True, minimal=True)
+    r = ref.dense_attention_backward(q, k, v, do, causal=True)
+    try:
+        for limit, want_path in ((None, ds_path), (0, rc_path), (1 << 40, ds_path)):
+            fa.set_backward_workspace_limit(limit)
+            qa, ka, va = (t.clone().requires_grad_() for t in (qd, kd, vd))
+            fa.tilelang_flash_attn_func(qa, ka, va, causal=True).backward(dod)
+            torch.cuda.synchronize()
+            for got, want, exact, name in zip((qa.grad, ka.grad, va.grad), r, want_path,
+                                              ("dq", "dk", "dv")):
+                assert torch.equal(got, exact), f"{name} (limit {limit}): not the chosen path"
+                assert_close(got, want, what=name)
+    finally:
+        fa.set_backward_workspace_limit(None)

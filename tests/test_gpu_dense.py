@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import tilelang_fa_v100 as fa
-from helpers import assert_close, assert_lse, randn, rel_l2
+from helpers import assert_close, assert_close_as_reference_arithmetic, assert_lse, randn, rel_l2
 from oracle import attention_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -246,13 +246,14 @@ def test_default_window_is_full_attention():
 
 
 def test_sliding_window_bf16_gradients():
-    """bf16 band: forward to the elementwise bar, gradients by relative L2.
+    """bf16 band: forward and gradients to the elementwise bar.
 
-    bf16 keeps 8 significant bits, and the backward's P and dS enter the
-    matrix products as bf16, so a key's dK / dV sums ~100 terms each carrying
-    ~2^-9 relative rounding; inside a narrow band P is large and single
-    elements can exceed atol 2e-3 / rtol 1e-2 (fp16 cases of the same shapes
-    meet it elementwise, see test_sliding_window_forward_and_backward).
+    bf16 keeps 8 significant bits, and the backward's P and scale·dS enter the
+    matrix products as bf16, as the reference's fp16 kernels round them
+    (_kernels_backward.py:74,160-167).  The gradients are held to the
+    north-star bar wherever the oracle's restatement of that arithmetic
+    (round_dtype=bfloat16) meets it, and otherwise to twice its error; the
+    relative L2 bound applies throughout.
     """
     g = torch.Generator().manual_seed(9)
     B, Sq, Sk, H, Hk, D, window = 2, 300, 520, 4, 4, 128, (64, 32)
@@ -266,7 +267,9 @@ def test_sliding_window_bf16_gradients():
     assert_lse(lse, r_lse)
     out.backward(do.to(DEV))
     r = ref.dense_attention_backward(q, k, v, do, window=window)
-    for got, want, name in zip((qd.grad, kd.grad, vd.grad), r, ("dq", "dk", "dv")):
+    r16 = ref.dense_attention_backward(q, k, v, do, window=window, round_dtype=dt)
+    for got, want, want16, name in zip((qd.grad, kd.grad, vd.grad), r, r16, ("dq", "dk", "dv")):
+        assert_close_as_reference_arithmetic(got, want, want16, what=name)
         assert rel_l2(got, want) < 1e-2, name
 
 
@@ -370,3 +373,23 @@ def test_deterministic_flag_changes_nothing(d):
     settings give the same gradients bit for bit."""
     res = _grads_both_flags(d, 23)
     assert all(torch.equal(x, y) for x, y in zip(res[0], res[1]))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_backward_beyond_65535_batch_heads(d):
+    """4100 x 16 (batch, head) pairs: every grid is one-dimensional, so the
+    backward takes what the forward takes (the former 65535 limit was a
+    leftover of a grid-y launch)."""
+    B, S, H = 4100, 16, 16
+    g = torch.Generator().manual_seed(31)
+    q, k, v, do = (randn(g, B, S, H, d) for _ in range(4))
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    print(f"B{B} S{S} H{H} D{d}", flush=True)
+    out = fa.tilelang_flash_attn_func(qd, kd, vd, causal=True)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    r_out, _ = ref.dense_attention(q, k, v, causal=True)
+    assert_close(out, r_out)
+    r = ref.dense_attention_backward(q, k, v, do, causal=True)
+    for got, want, name in zip((qd.grad, kd.grad, vd.grad), r, ("dq", "dk", "dv")):
+        assert_close(got, want, what=name)

@@ -137,6 +137,40 @@ def test_backward_matches_autograd_fp64():
         torch.testing.assert_close(dv, gv, atol=1e-10, rtol=1e-9)
 
 
+def test_backward_rounding_restatement():
+    """round_dtype restates the reference's 16-bit roundings.  Rounding to
+    the compute dtype itself changes nothing (so the formula is the pinned
+    exact one).  With one query row, head_dim 1, q = 1 and dO = 1, dK[j] is
+    the rounded scale*dS[j] and dV[j] the rounded P[j] themselves, so they
+    must be fp16 values equal to an independent restatement that rounds
+    scale*dS (not dS) and P, with rowdot from the rounded output."""
+    g = torch.Generator().manual_seed(12)
+    q, k, v, do = (torch.randn(2, 9, 4, 8, generator=g).half() for _ in range(4))
+    k, v = k[:, :, :2].contiguous(), v[:, :, :2].contiguous()
+    for causal in (False, True):
+        exact = ref.dense_attention_backward(q, k, v, do, 0.3, causal)
+        same = ref.dense_attention_backward(q, k, v, do, 0.3, causal, round_dtype=torch.float32)
+        for a, b in zip(exact, same):
+            assert torch.equal(a, b)
+    scale = 0.7
+    q1 = torch.ones(1, 1, 1, 1)
+    k1 = torch.tensor([0.3, -1.2, 2.5, 0.9, -0.4]).view(1, 5, 1, 1)
+    v1 = torch.tensor([1.7, -0.6, 0.2, 3.1, -2.2]).view(1, 5, 1, 1)
+    do1 = torch.ones(1, 1, 1, 1)
+    dq, dk, dv = ref.dense_attention_backward(q1, k1, v1, do1, scale, False,
+                                              round_dtype=torch.float16)
+    s = k1.view(5) * scale
+    p = torch.softmax(s, 0)
+    o = (p * v1.view(5)).sum().half().float()
+    want_ds = (p * (v1.view(5) - o) * scale).half().float()
+    want_p = p.half().float()
+    assert torch.equal(dk.view(5), want_ds)
+    assert torch.equal(dv.view(5), want_p)
+    assert torch.equal(dk.view(5), dk.view(5).half().float())
+    # rounding dS before the scale gives different values here
+    assert not torch.equal(want_ds, (p * (v1.view(5) - o)).half().float() * scale)
+
+
 # ------------------------------------------------------------------ integer parts (bit-exact)
 
 def test_paged_rows_resolve_every_slot():

@@ -4,9 +4,9 @@ The allocation-free entry point runs the same validation and kernels as
 fa_paged_decode with the split-KV workspace taken from the library's static
 per-device scratch array, so on the same inputs its output and LSE must be
 bit-identical to the workspace entry point's.  Two calls in a row, the second
-with a smaller problem (the array keeps the first call's contents), and
-problems on both decode kernels (head_dim 128 streaming, head_dim 64 / 256
-chunked).
+with a smaller problem (the array keeps the first call's contents), at
+head_dim 128 and at head_dim 256 then 64 (all on the streaming decode
+kernel).
 """
 import ctypes
 

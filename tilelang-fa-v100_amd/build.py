@@ -50,7 +50,6 @@ COMMON_FLAGS = [
     "-mcode-object-version=5",
     # Packed FP32 instructions are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-munsafe-fp-atomics",
     "-Wno-unused-result",
     f"-I{INCLUDE}",
     f"-I{CSRC}",

@@ -5,7 +5,7 @@
 // (:88-176).  The reference recomputes QK^T and dO V^T in both kernels (7
 // GEMMs per tile pair); here one KV-stationary kernel does the 5 GEMMs
 //   S = Q K^T,  dP = dO V^T,  dV += P^T dO,  dK += dS^T Q,  dQ += dS K
-// with P = exp(scale*S - lse), dS = P * (dP - rowdot(O, dO))
+// with P = exp(scale*S - lse), dS = P * (dP - rowdot(O, dO)) * scale
 // (_kernels_backward.py:72-74,159-170).  dQ comes from a query-stationary
 // kernel (fa_bwd_dq.h) that recomputes S and dP per query tile and builds
 // each dQ row in one wave, like the reference's dQ kernel: no atomics, so
@@ -15,11 +15,14 @@
 //
 // Kernels, in launch order:
 //   bwd_dq_kernel       dQ (fa_bwd_dq.h); also writes the row statistics
-//                       rowdot(O, dO) and LSE*log2(e) of the rows it owns
-//                       into one array [B*H][2][Sq] (LSE*log2(e) first,
-//                       rowdot second), so a lane of the dK / dV kernels
-//                       addresses either with a 32-bit offset from a
+//                       scale·rowdot(O, dO) and LSE*log2(e) of the rows it
+//                       owns into one array [B*H][2][Sq] (LSE*log2(e)
+//                       first, scale·rowdot second), so a lane of the dK / dV
+//                       kernels addresses either with a 32-bit offset from a
 //                       per-head base.
+// Every kernel forms dS already multiplied by softmax_scale and rounds that
+// to 16 bits before its products, as the reference does
+// (_kernels_backward.py:74,160), so dS has fp16's full range.
 //   bwd_main_kernel     head_dim 64 dK / dV: workgroup = 128 keys (32 per
 //                       wave) of one KV head; loops over the 64-row query
 //                       tiles of every query head that shares the KV head
@@ -28,7 +31,7 @@
 // At head_dim 128 / 256 with causal or full attention and a workspace of
 // bwd_workspace_bytes, the order is instead bwd_stats_kernel (the row
 // statistics), bwd_main_mfma_kernel<..., DS = true> (dK / dV, storing its dS
-// tiles) and bwd_dq_ds_kernel (dQ = scale · dS K from them), fa_bwd_ds.h.
+// tiles) and bwd_dq_ds_kernel (dQ = dS K from them), fa_bwd_ds.h.
 #include "fa_bwd_dq.h"
 #include "fa_bwd_ds.h"
 #include "fa_bwd_mfma.h"
@@ -86,6 +89,7 @@ __global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const f
   const int kv0w = kv0 + 32 * wave;
   const int my_kv = kv0w + lr;
   const float scale_log2 = a.softmax_scale * kLog2e;
+  const float sc = a.softmax_scale;
 
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
@@ -221,7 +225,9 @@ __global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const f
               p = vis ? p : 0.f;
             }
             s[qt][i] = p;                       // P
-            dp[qt][i] = p * (dp[qt][i] - d4[r]);  // dS (unscaled)
+            // scale·dS, rounded to 16 bits as the reference does
+            // (_kernels_backward.py:160); d4 holds scale·rowdot.
+            dp[qt][i] = p * fmaf(dp[qt][i], sc, -d4[r]);
           }
         }
       // Pack P and dS as B operands.
@@ -260,15 +266,14 @@ __global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const f
                     (int64_t)my_kv * a.dk_stride[1] + hk * a.dk_stride[2];
     uint16_t* dvp = static_cast<uint16_t*>(a.dv) + b * a.dv_stride[0] +
                     (int64_t)my_kv * a.dv_stride[1] + hk * a.dv_stride[2];
-    const float sc = a.softmax_scale;
 #pragma unroll
     for (int dt = 0; dt < S::DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * dt + 8 * g + 4 * lh;
         u32x2 wk, wv;
-        wk[0] = T::pack(dk[dt][4 * g] * sc, dk[dt][4 * g + 1] * sc);
-        wk[1] = T::pack(dk[dt][4 * g + 2] * sc, dk[dt][4 * g + 3] * sc);
+        wk[0] = T::pack(dk[dt][4 * g], dk[dt][4 * g + 1]);
+        wk[1] = T::pack(dk[dt][4 * g + 2], dk[dt][4 * g + 3]);
         wv[0] = T::pack(dv[dt][4 * g], dv[dt][4 * g + 1]);
         wv[1] = T::pack(dv[dt][4 * g + 2], dv[dt][4 * g + 3]);
         st8(dkp + d, wk);
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void bwd_main_kernel(fa_bwd_args a, const f
 
 // ----------------------------------------------------------------- launchers
 
-// Workspace: the row statistics [B*H][2][Sq] (LSE*log2(e), rowdot), then,
+// Workspace: the row statistics [B*H][2][Sq] (LSE*log2(e), scale·rowdot), then,
 // for the dS-store path, the dS tiles (fa_bwd_ds.h) from byte ds_offset(a).
 static size_t stats_bytes(const fa_bwd_args& a) {
   const size_t rows = (size_t)a.batch * a.seqlen_q * a.num_heads;
@@ -288,7 +293,7 @@ static size_t stats_bytes(const fa_bwd_args& a) {
 static size_t ds_offset(const fa_bwd_args& a) { return (stats_bytes(a) + 255) & ~(size_t)255; }
 
 // Bytes of dS tiles for the dS-store path, or 0 where it does not apply:
-// head_dim 128 / 256, causal or full attention, at most tiles::kBwdDsMaxBytes.
+// head_dim 128 / 256, causal or full attention, below tiles::kBwdDsMaxBytes.
 static size_t ds_bytes(const fa_bwd_args& a) {
   const int mode = mask_mode(a);
   if ((a.head_dim != 128 && a.head_dim != 256) || mode == kMaskBand || a.seqlen_q <= 0 ||
@@ -297,7 +302,9 @@ static size_t ds_bytes(const fa_bwd_args& a) {
   const DsTiles L = mode == kMaskCausal ? ds_tiles<kMaskCausal>(a.seqlen_q, a.seqlen_k)
                                         : ds_tiles<kMaskNone>(a.seqlen_q, a.seqlen_k);
   const size_t bytes = 2048 * (size_t)a.batch * a.num_heads * (size_t)L.per_head();
-  return bytes <= tiles::kBwdDsMaxBytes ? bytes : 0;
+  // Strictly below the cap: a wave's dS reads go through one buffer resource
+  // of count(qt) * 2 KB bytes (a 32-bit size), and count(qt) <= per_head.
+  return bytes < tiles::kBwdDsMaxBytes ? bytes : 0;
 }
 
 size_t bwd_min_workspace_bytes(const fa_bwd_args& a) { return stats_bytes(a); }
@@ -366,7 +373,7 @@ static void launch_bwd_dq(const fa_bwd_args& a, int mode, float* stats, hipStrea
 }
 
 // dS-store path (head_dim 128 / 256): row statistics, dK / dV storing dS,
-// then dQ = scale · dS K.
+// then dQ = dS K (dS includes the scale).
 template <class T, int D>
 static hipError_t launch_bwd_ds(const fa_bwd_args& a, int mode, void* ws, hipStream_t st) {
   float* stats = static_cast<float*>(ws);

@@ -11,11 +11,13 @@
 // registers:
 //   Sᵀ  = K Qᵀ      (A = K rows from LDS, B = the wave's Q rows in registers)
 //   dPᵀ = V dOᵀ     (A = V rows from LDS, B = the wave's dO rows)
-//   P = exp2(Sᵀ·scale·log2e − LSE·log2e),  dSᵀ = P (dPᵀ − rowdot)
+//   P = exp2(Sᵀ·scale·log2e − LSE·log2e),  dSᵀ = P (dPᵀ − rowdot)·scale
+//   (rounded to 16 bits with the scale in, as the reference does,
+//   _kernels_backward.py:74)
 //   dQᵀ += Kᵀ dSᵀ   (A = Kᵀ by ds_read_b64_tr_b16 from the same K tile,
 //                    B = dSᵀ packed straight from the accumulators)
 // A lane's scores all belong to its own query row (column lr of Sᵀ), so the
-// row statistics (LSE·log2e, rowdot, computed here) are one register
+// row statistics (LSE·log2e, scale·rowdot, computed here) are one register
 // each.  K and V tiles go HBM -> LDS with global_load_lds_dwordx4 (every
 // wave loads BPW 1 KB blocks of each, two tiles in flight), rows stored
 // with the 16-byte chunk swizzle of fa_fwd_d128.h.
@@ -71,6 +73,7 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 31, lh = lane >> 5;
   const float scale_log2 = a.softmax_scale * kLog2e;
+  const float sc = a.softmax_scale;
 
   const int row_last = min(row0 + S::BM, Sq) - 1;
   const int wg_lo = kv_lo(row0), wg_hi = kv_hi(row_last);
@@ -89,8 +92,8 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
   // ---- this lane's query row: Q and dO as B operands, and its statistics,
   // computed here and stored for the dK / dV kernel, which runs after this
   // one: LSE·log2(e) (+inf for a row that saw no key, and for rows past Sq,
-  // so that P is exactly zero) and rowdot = Σ_d O·dO (the reference's
-  // row_dot, _kernels_backward.py:203).  Lanes l and l + 32 hold the two
+  // so that P is exactly zero) and scale·rowdot, rowdot = Σ_d O·dO (the
+  // reference's row_dot, _kernels_backward.py:203).  Lanes l and l + 32 hold the two
   // halves of each 16-column chunk of the row.
   u32x4 qf[D / 16], df[D / 16];
   float lse2 = __builtin_inff(), rdot = 0.f;
@@ -115,7 +118,7 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
     if (row_valid) {
       const float l = a.lse[(int64_t)bh * Sq + row];
       lse2 = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
-      rdot = full;
+      rdot = full * sc;
       if (lh == 0) {
         float* st = stats + 2 * (int64_t)bh * Sq;
         st[row] = lse2;
@@ -231,7 +234,7 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
 #pragma unroll
         for (int i = EPC * (D / 16); i < 16; ++i) prob(i);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dp[i] = s[i] * (dp[i] - rdot);
+        for (int i = 0; i < 16; ++i) dp[i] = s[i] * fmaf(dp[i], sc, -rdot);
       };
       if (need_mask)
         probs(BoolC<true>{});
@@ -283,13 +286,12 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
     compute_tile((j + 1) * BN, k1, v1);
   }
 
-  // ---- dQ = scale · Σ dS K; acc[dt][4g + r] = dQ[row][32dt + 8g + 4lh + r].
+  // ---- dQ = Σ dS K; acc[dt][4g + r] = dQ[row][32dt + 8g + 4lh + r].
   if constexpr (D == 256) {
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) agpr_fence_out(acc[dt]);
   }
   if (!row_valid) return;
-  const float sc = a.softmax_scale;
   uint16_t* dqp = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] +
                   (int64_t)row * a.dq_stride[1] + h * a.dq_stride[2];
 #pragma unroll
@@ -297,8 +299,8 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       u32x2 w;
-      w[0] = T::pack(acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc);
-      w[1] = T::pack(acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc);
+      w[0] = T::pack(acc[dt][4 * g], acc[dt][4 * g + 1]);
+      w[1] = T::pack(acc[dt][4 * g + 2], acc[dt][4 * g + 3]);
       st8(dqp + 32 * dt + 8 * g + 4 * lh, w);
     }
 }

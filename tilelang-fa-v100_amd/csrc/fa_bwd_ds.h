@@ -1,11 +1,11 @@
 // dQ of the dense attention backward from stored dS tiles (head_dim 128 and
 // 256, causal or full attention).
 //
-// The key-stationary dK / dV kernel (fa_bwd_mfma.h) forms dS = P (dP − rowdot)
-// for every (query tile, key block) pair it visits.  With its DS variant it
-// also stores each wave's 32 x 32 block of dS (the 16-bit B operand of its
-// dKᵀ product, 2 KB) to the workspace, and dQ = scale · dS K becomes one
-// product per tile pair (bwd_dq_ds_kernel) instead of the three of
+// The key-stationary dK / dV kernel (fa_bwd_mfma.h) forms dS = P (dP −
+// rowdot)·scale for every (query tile, key block) pair it visits.  With its
+// DS variant it also stores each wave's 32 x 32 block of dS (the 16-bit B
+// operand of its dKᵀ product, 2 KB) to the workspace, and dQ = dS K becomes
+// one product per tile pair (bwd_dq_ds_kernel) instead of the three of
 // bwd_dq_kernel (fa_bwd_dq.h), which recomputes S and dP.  The price is
 // writing and reading dS once through HBM (2 bytes per visible (query, key)
 // pair).  Every dQ element is still summed by one lane over the keys in a
@@ -80,8 +80,9 @@ __host__ __device__ inline DsTiles ds_tiles(int sq, int sk) {
 }
 
 // Row statistics [B*H][2][Sq] fp32 for the dK / dV kernel: LSE·log2(e) (+inf
-// for a row that saw no key, so that P is exactly zero) and rowdot = Σ_d O·dO
-// (the reference's row_dot, _kernels_backward.py:203), with the arithmetic
+// for a row that saw no key, so that P is exactly zero) and scale·rowdot,
+// rowdot = Σ_d O·dO (the reference's row_dot, _kernels_backward.py:203), with
+// the arithmetic
 // bwd_dq_kernel uses when it writes them: lanes l and l + 32 each sum half of
 // every 16-column chunk with v_dot2, then the two halves are added.  One wave
 // per 32 rows of a head.
@@ -114,11 +115,11 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(fa_bwd_args a, float* st
   if (row < Sq && lh == 0) {
     float* st = stats + 2 * (int64_t)bh * Sq;
     st[row] = (l == neg_inf()) ? __builtin_inff() : l * kLog2e;
-    st[Sq + row] = full;
+    st[Sq + row] = full * a.softmax_scale;
   }
 }
 
-// dQ = scale · Σ_kb dS(qt, kb) K(kb) for head_dim 128 / 256.  Workgroup: 8
+// dQ = Σ_kb dS(qt, kb) K(kb) for head_dim 128 / 256 (dS carries the scale).  Workgroup: 8
 // waves, wave w owns query tile qt = 8 qb + w of one query head; steps run
 // over 32-key blocks.  Per step, wave w copies rows 4w..4w+3 of the K tile
 // and its own 2 KB dS tile HBM -> LDS (buffer DMA: K rows past Sk and dS
@@ -272,10 +273,9 @@ __global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_
   }
   wait_vmem();
 
-  // acc[dt][4g + r] = dQ[32qt + lr][32dt + 8g + 4lh + r] / scale.
+  // acc[dt][4g + r] = dQ[32qt + lr][32dt + 8g + 4lh + r].
   const int row = 32 * qt + lr;
   if (qt >= L.nq || row >= Sq) return;
-  const float sc = a.softmax_scale;
   uint16_t* dqp = static_cast<uint16_t*>(a.dq) + b * a.dq_stride[0] +
                   (int64_t)row * a.dq_stride[1] + h * a.dq_stride[2];
 #pragma unroll
@@ -283,8 +283,8 @@ __global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       u32x2 w;
-      w[0] = T::pack(acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc);
-      w[1] = T::pack(acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc);
+      w[0] = T::pack(acc[dt][4 * g], acc[dt][4 * g + 1]);
+      w[1] = T::pack(acc[dt][4 * g + 2], acc[dt][4 * g + 3]);
       st8(dqp + 32 * dt + 8 * g + 4 * lh, w);
     }
 }

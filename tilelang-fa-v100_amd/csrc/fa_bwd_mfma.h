@@ -2,7 +2,9 @@
 //
 // Same mathematics as bwd_main_kernel (fa_bwd.hip): per (key tile, query
 // tile) the products S = Q Kᵀ, dP = dO Vᵀ, dVᵀ += dOᵀ P and dKᵀ += Qᵀ dS, with
-// P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot); dQ comes from
+// P = exp2(S·scale·log2e − LSE·log2e) and dS = P (dP − rowdot)·scale (rounded
+// to 16 bits with the scale in, as the reference does,
+// tilelang_fa_v100/_kernels_backward.py:160); dQ comes from
 // the query-stationary bwd_dq_kernel (fa_bwd_dq.h).  Layout, for the gfx950
 // memory instructions:
 //  * D = 128: 256 keys per workgroup, 8 waves x 32 keys (two waves per SIMD),
@@ -89,6 +91,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
   const int wrow = 32 * wave;  // first key row of the wave within the tile
   const int kvw = kv0 + wrow;
   const float scale_log2 = a.softmax_scale * kLog2e;
+  const float sc = a.softmax_scale;
 
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
@@ -276,7 +279,8 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     const int wkv_last = min(kvw + 31, Sk - 1);
     const bool need_mask = (CAUSAL && !band.all(i0, i0 + S::BQ - 1, kvw, wkv_last)) ||
                            (kvw + 32 > Sk) || (i0 + S::BQ > Sq);
-    // P = exp2(S·scale·log2e − lse2), dS = P (dP − rowdot).  Element (g, r)
+    // P = exp2(S·scale·log2e − lse2), dS = P (dP·scale − scale·rowdot).  The
+    // statistics hold scale·rowdot, so the scale costs nothing.  Element (g, r)
     // is query i0 + 8g + 4lh + r; on masked tiles it sees the lane's key iff
     // c = 8g + r lies in [t_lo, t_hi); masked elements get P = 0.  The
     // masked and unmasked forms are separate code paths so that the uniform
@@ -304,7 +308,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
             p = (c >= t_lo && c < t_hi) ? p : 0.f;
           }
           s[i] = p;
-          dp[i] = p * (dp[i] - d4[r]);
+          dp[i] = p * fmaf(dp[i], sc, -d4[r]);
         }
       }
     };
@@ -417,7 +421,6 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     }
   }
 
-  const float sc = a.softmax_scale;
   const int my_kv = kvw + lr;
   if (my_kv >= Sk) return;
   uint16_t* dkp = static_cast<uint16_t*>(a.dk) + b * a.dk_stride[0] +
@@ -430,8 +433,8 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     for (int g = 0; g < 4; ++g) {
       const int d = 32 * dt + 8 * g + 4 * lh;
       u32x2 wk, wv;
-      wk[0] = T::pack(dk[dt][4 * g] * sc, dk[dt][4 * g + 1] * sc);
-      wk[1] = T::pack(dk[dt][4 * g + 2] * sc, dk[dt][4 * g + 3] * sc);
+      wk[0] = T::pack(dk[dt][4 * g], dk[dt][4 * g + 1]);
+      wk[1] = T::pack(dk[dt][4 * g + 2], dk[dt][4 * g + 3]);
       wv[0] = T::pack(dv[dt][4 * g], dv[dt][4 * g + 1]);
       wv[1] = T::pack(dv[dt][4 * g + 2], dv[dt][4 * g + 3]);
       st8(dkp + d, wk);

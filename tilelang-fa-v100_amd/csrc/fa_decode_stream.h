@@ -1,5 +1,6 @@
-// Persistent streaming split-KV decode for head_dim 64 / 128 / 256 / 512
-// (gfx950).
+// Persistent streaming split-KV decode for head_dim 64 / 128 / 256 and pages
+// of at least 16 keys (gfx950); head_dim 512 and smaller pages take the
+// chunked decode_split_kernel (fa_decode.hip).
 //
 // Work item = (sequence b, KV head, group of GB query heads, split c), one
 // split being kSplit consecutive keys.  Items are numbered sequence-major,

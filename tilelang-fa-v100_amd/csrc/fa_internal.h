@@ -16,7 +16,7 @@ namespace fa {
 hipError_t launch_fwd(const fa_fwd_args& a, hipStream_t st);
 
 // bwd_workspace_bytes: the dS-store path's workspace where it applies
-// (head_dim 128, causal or full attention, dS tiles within
+// (head_dim 128 or 256, causal or full attention, dS tiles below
 // tiles::kBwdDsMaxBytes), else the row statistics only.
 // bwd_min_workspace_bytes: the row statistics (the recompute path).
 size_t bwd_workspace_bytes(const fa_bwd_args& a);
@@ -38,8 +38,8 @@ int device_cu_count();
 
 // Grid of a persistent launch over ntiles x nbh tiles (persistent_tile in
 // fa_common.h): per_cu workgroups per CU, fewer when there are fewer tiles,
-// a multiple of 8 when nbh is one (each workgroup then stays on one XCD's
-// heads).
+// a multiple of 8 when nbh is a multiple of 8 (each workgroup then stays on
+// one XCD's heads).
 inline int persistent_grid(int ntiles, int nbh, int per_cu) {
   const int64_t total = (int64_t)ntiles * nbh;
   int64_t w = std::min<int64_t>(total, (int64_t)per_cu * device_cu_count());

@@ -60,6 +60,19 @@ constexpr int kFwdCoreKeys512 = 32;
 // with three Q / dO buffers 1.115 against 1.105 ms for the kernel (it runs
 // near the LDS read rate: five 1 KB operand reads per four MFMAs).
 constexpr int kBwdQueryRows = 32;
+// Measured again with the current kernel (same box, T1 backward, dK / dV /
+// dQ bit-identical in every variant): 4 waves x 64 keys at one wave per SIMD
+// (dK / dV of 64 keys pinned in the 256 AGPRs, every Q / dO / Qᵀ / dOᵀ read
+// feeding two products) 1.85 ms against 1.69-1.77 ms for 8 waves x 32 keys,
+// and C2 0.29 against 0.26-0.27 ms.  Counters (T1): the same MFMA busy
+// cycles but co-execution of MFMA and VALU 10x lower (3.0e7 against 2.9e8
+// cycles): a lone wave issues in order, so its softmax runs between its
+// products instead of under the partner wave's.  Interleaving the element
+// work into the chains (exponentials between the dP products, dS between the
+// dV products, separate S / dP / dV / dK chains) compiled without spills
+// only with the masked / unmasked branch confined to the element work, and
+// still measured 1.81-1.93 ms (head_dim 256, same schedule: 1.76-1.87
+// against 1.64-1.70 ms for the combined S / dP loop and dV / dK chain).
 
 // ---- backward: dQ (fa_bwd_dq.h), query-stationary, no atomics.  Evidence
 // (fa_bwd per call, ms, dQ by fp32 atomics from the key-stationary kernel /

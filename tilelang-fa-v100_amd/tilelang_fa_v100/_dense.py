@@ -9,6 +9,7 @@ reference's permute/contiguous copies (interface.py:19-21,38,51) are gone.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -99,6 +100,90 @@ def bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, determi
     return a
 
 
+# ---- backward workspace policy
+#
+# fa_bwd runs one of two paths, chosen by the workspace it is given:
+#  * fa_bwd_min_workspace_bytes: the row statistics only (8 bytes per query
+#    row and head); dQ recomputes S and dP, like the reference's dQ kernel.
+#    This is the memory footprint of the reference's tilelang_backward
+#    (_kernels_backward.py:200-208: row_dot plus its fp32 up-casts).
+#  * fa_bwd_workspace_bytes: at head_dim 128 / 256 with causal or full
+#    attention, the statistics plus the dS tiles (2 bytes per visible
+#    (query, key) pair: 268 MB at [4, 2048, 16, 128], 2.15 GB at
+#    [2, 8192, 16, 128]); dQ then costs one product per tile pair instead of
+#    three.
+# The dS path is taken while its workspace fits the limit below, and the
+# recompute path whenever it does not or its allocation fails, so the
+# backward never needs more memory than the reference's.
+
+WORKSPACE_LIMIT_ENV = "TILELANG_FA_BWD_WORKSPACE_LIMIT"
+# Default limit: this share of the memory the device can still hand out
+# (free device memory plus blocks torch holds cached but unused), or all of
+# the cached blocks when they alone hold the dS workspace.
+FREE_MEMORY_SHARE = 0.5
+_workspace_limit = None
+
+
+def set_backward_workspace_limit(nbytes):
+    """Caps the dense backward's workspace at `nbytes` bytes (0: always the
+    recompute path); None restores the default.  The environment variable
+    TILELANG_FA_BWD_WORKSPACE_LIMIT (bytes) sets it too; this call wins."""
+    global _workspace_limit
+    if nbytes is not None:
+        nbytes = int(nbytes)
+        if nbytes < 0:
+            raise ValueError(f"workspace limit must be >= 0, got {nbytes}")
+    _workspace_limit = nbytes
+
+
+def workspace_limit(device, want=None) -> int:
+    """Bytes the backward's workspace may take on `device` right now.
+
+    want: the dS workspace's size.  When torch already holds at least that
+    much cached but unused (the steady state of a training loop, which frees
+    the workspace after every backward), the workspace comes from those
+    blocks and the device is not queried: torch.cuda.mem_get_info took ~5 us
+    on an idle MI355X and a median of ~90 us behind a busy stream."""
+    if _workspace_limit is not None:
+        return _workspace_limit
+    env = os.environ.get(WORKSPACE_LIMIT_ENV)
+    if env:
+        try:
+            return max(int(env), 0)
+        except ValueError:
+            raise ValueError(f"{WORKSPACE_LIMIT_ENV} must be a byte count, got {env!r}") from None
+    cached = max(torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device), 0)
+    if want is not None and want <= cached:
+        return cached
+    free, _ = torch.cuda.mem_get_info(device)
+    return int((free + cached) * FREE_MEMORY_SHARE)
+
+
+def choose_workspace(full: int, minimal: int, limit: int) -> int:
+    """Workspace bytes to ask for: `full` (dS path) when it is larger than
+    `minimal` and fits `limit`, else `minimal` (recompute path)."""
+    return full if minimal < full <= limit else minimal
+
+
+def _empty_bytes(n: int, device):
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def alloc_workspace(full: int, minimal: int, device):
+    """The backward's workspace tensor: the dS path's when the limit allows
+    it, falling back to the recompute path's when that allocation raises
+    torch.cuda.OutOfMemoryError."""
+    if full <= minimal:
+        return _empty_bytes(minimal, device)
+    n = choose_workspace(full, minimal, workspace_limit(device, full))
+    if n == minimal:
+        return _empty_bytes(minimal, device)
+    try:
+        return _empty_bytes(n, device)
+    except torch.cuda.OutOfMemoryError:
+        return _empty_bytes(minimal, device)
+
+
 def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
              deterministic: bool = False, window=(-1, -1)):
     """Returns (dq, dk, dv), each contiguous [B, S, H, D] in q's dtype."""
@@ -112,10 +197,12 @@ def backward(q, k, v, out, dout, lse, softmax_scale: float, causal: bool,
     a = bwd_args(q, k, v, out, dout, lse, dq, dk, dv, softmax_scale, causal, deterministic,
                  window)
     lib = _lib.load()
-    nbytes = lib.fa_bwd_workspace_bytes(ctypes.byref(a))
-    if nbytes == 0:
+    full = lib.fa_bwd_workspace_bytes(ctypes.byref(a))
+    minimal = lib.fa_bwd_min_workspace_bytes(ctypes.byref(a))
+    if full == 0 or minimal == 0:
         _lib.check(_lib.FA_E_INVALID, "fa_bwd_workspace_bytes")
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    ws = alloc_workspace(full, minimal, q.device)
+    nbytes = ws.numel()
     _lib.check(_lib.call_on(q.device, lambda st: lib.fa_bwd(ctypes.byref(a), ws.data_ptr(),
                                                             nbytes, st)), "fa_bwd")
     return dq, dk, dv
