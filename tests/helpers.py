@@ -61,21 +61,40 @@ def assert_close(got, ref, atol=ATOL, rtol=RTOL, what="out"):
 
 def assert_close_as_reference_arithmetic(got, ref, ref_rounded, what="grad", norm=1.0):
     """Gradient check against the exact fp32 gradient `ref` (all three divided
-    by `norm`, e.g. a loss scale): the north-star elementwise bar wherever
+    by `norm`, e.g. a loss scale), element by element: within the north-star
+    bound atol + rtol·|ref|, or within twice the largest error of
     `ref_rounded` - the oracle's restatement of the reference's own 16-bit
-    roundings (dense_attention_backward(..., round_dtype=...)) - meets it;
-    if that restatement itself misses the bar somewhere, the kernel's largest
-    error may not exceed twice the restatement's largest error."""
+    roundings (dense_attention_backward(..., round_dtype=...)) - where that
+    is larger.  The restatement's errors land on different elements than
+    the kernel's (its roundings differ in the last bit here and there), so its
+    largest error, not its error at the same element, sets the floor."""
     got = got.float().cpu() / norm
     ref = ref.float().cpu() / norm
-    ref_err = (ref_rounded.float().cpu() / norm - ref).abs()
-    if bool((ref_err <= ATOL + RTOL * ref.abs()).all()):
-        assert_close(got, ref, what=what)
-        return
+    floor = 2 * (ref_rounded.float().cpu() / norm - ref).abs().max().item()
     assert torch.isfinite(got).all(), f"{what}: non-finite values"
-    err = (got - ref).abs().max().item()
-    assert err <= 2 * ref_err.max().item(), \
-        f"{what}: max err {err:.3e}, reference arithmetic {ref_err.max().item():.3e}"
+    err = (got - ref).abs()
+    bound = torch.clamp(ATOL + RTOL * ref.abs(), min=floor)
+    bad = err > bound
+    if bad.any():
+        idx = bad.nonzero()[0].tolist()
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} elements out of tolerance; max abs err "
+            f"{err.max().item():.3e} (reference arithmetic floor {floor:.3e}); first bad "
+            f"{idx}: got {got[tuple(idx)].item():.6f} ref {ref[tuple(idx)].item():.6f}")
+
+
+def standard_forward_batch(B, H, Sq, D):
+    """Batch size (at least B) from which the dense forward of [B', Sq, H, D]
+    runs on the row-tile cores rather than the key-split kernel: their grid,
+    ceil(Sq / rows) x B' x H workgroups (rows = 128 at head_dim 64, 256 at
+    head_dim 128), reaches half the CUs (csrc/fa_tiles.h kFwdSplitMaxFill).
+    Head_dim 256 always runs on the row-tile core."""
+    if D not in (64, 128):
+        return B
+    rows = 128 if D == 64 else 256
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    per_batch = math.ceil(Sq / rows) * H
+    return max(B, math.ceil(math.ceil(cus / 2) / per_batch))
 
 
 def rel_l2(got, ref):

@@ -10,7 +10,8 @@ import pytest
 import torch
 
 import tilelang_fa_v100 as fa
-from helpers import assert_close, assert_close_as_reference_arithmetic, assert_lse, randn, rel_l2
+from helpers import (assert_close, assert_close_as_reference_arithmetic, assert_lse, randn, rel_l2,
+                     standard_forward_batch)
 from oracle import attention_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -43,15 +44,28 @@ def _ids(c):
     return f"B{B}-{Sq}x{Sk}-H{H}/{Hk}-D{D}-{'c' if causal else 'nc'}-{str(dt)[6:]}"
 
 
-@pytest.mark.parametrize("case", FWD_CASES, ids=[_ids(c) for c in FWD_CASES])
-def test_forward_matches_oracle(case):
+# Head_dim 64 / 128 cases also run with the batch repeated until the row-tile
+# cores take them (head_dim 256 always runs on its row-tile core).
+FWD_RUNS = [(c, "as_given") for c in FWD_CASES] + \
+    [(c, "row_tiles") for c in FWD_CASES if c[5] in (64, 128)]
+
+
+@pytest.mark.parametrize("case,grid", FWD_RUNS, ids=[f"{_ids(c)}-{g}" for c, g in FWD_RUNS])
+def test_forward_matches_oracle(case, grid):
+    """grid: the case as listed (small batches at head_dim 64 / 128 take the
+    key-split kernel), or its batch repeated until the row-tile cores run
+    it; the oracle then checks the first two and the last batch."""
     B, Sq, Sk, H, Hk, D, causal, dt = case
+    if grid == "row_tiles":
+        B = standard_forward_batch(B, H, Sq, D)
     g = torch.Generator().manual_seed(0)
     q, k, v = randn(g, B, Sq, H, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt), randn(g, B, Sk, Hk, D, dtype=dt)
     out, lse, _ = fa.tilelang_flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal,
                                               return_attn_probs=True)
-    r_out, r_lse = ref.dense_attention(q, k, v, causal=causal)
     assert out.dtype == dt and out.shape == q.shape
+    pick = sorted({0, 1, B - 1} & set(range(B)))
+    q, k, v, out, lse = q[pick], k[pick], v[pick], out[pick], lse[pick]
+    r_out, r_lse = ref.dense_attention(q, k, v, causal=causal)
     assert_close(out, r_out)
     assert_lse(lse, r_lse)
     assert rel_l2(out, r_out) < 1e-2
@@ -250,10 +264,10 @@ def test_sliding_window_bf16_gradients():
 
     bf16 keeps 8 significant bits, and the backward's P and scale·dS enter the
     matrix products as bf16, as the reference's fp16 kernels round them
-    (_kernels_backward.py:74,160-167).  The gradients are held to the
-    north-star bar wherever the oracle's restatement of that arithmetic
-    (round_dtype=bfloat16) meets it, and otherwise to twice its error; the
-    relative L2 bound applies throughout.
+    (_kernels_backward.py:74,160-167).  Each gradient element is held to the
+    north-star bound or to twice the largest error of the oracle's
+    restatement of that arithmetic (round_dtype=bfloat16; ~4.4e-3 here),
+    whichever is larger; the relative L2 bound applies throughout.
     """
     g = torch.Generator().manual_seed(9)
     B, Sq, Sk, H, Hk, D, window = 2, 300, 520, 4, 4, 128, (64, 32)

@@ -20,7 +20,7 @@ import torch
 
 import tilelang_fa_v100 as fa
 from helpers import (assert_equal_rows, build_paged, needle_expected, needle_keys,
-                     needle_query, needle_scale)
+                     needle_query, needle_scale, standard_forward_batch)
 from oracle import attention_ref as ref
 from tilelang_fa_v100._paged_adapter import paged_forward_splits
 
@@ -77,11 +77,19 @@ def _dids(c):
     return f"{Sq}x{Sk}-H{H}/{Hk}-D{D}-{'c' if causal else 'nc'}-w{w[0]}_{w[1]}-{str(dt)[6:]}"
 
 
+DENSE_RUNS = [(c, "as_given") for c in DENSE] + [(c, "row_tiles") for c in DENSE if c[5] in (64, 128)]
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("sign", SIGNS, ids=_sid)
-@pytest.mark.parametrize("case", DENSE, ids=[_dids(c) for c in DENSE])
-def test_dense_mask_edges_bit_exact(case, sign):
+@pytest.mark.parametrize("case,grid", DENSE_RUNS, ids=[f"{_dids(c)}-{g}" for c, g in DENSE_RUNS])
+def test_dense_mask_edges_bit_exact(case, grid, sign):
+    """grid: the case as listed (at head_dim 64 / 128 these small batches
+    leave the row-tile cores too few workgroups, so the key-split kernel runs
+    them), or with its batch repeated until the row-tile cores run it."""
     B, Sq, Sk, H, Hk, D, causal, window, dt = case
+    if grid == "row_tiles":
+        B = standard_forward_batch(B, H, Sq, D)
     g = torch.Generator().manual_seed(11)
     q = needle_query(B * Sq, H, D, sign, dt).view(B, Sq, H, D)
     k = torch.stack([needle_keys(g, Sk, Hk, D, dt) for _ in range(B)])
@@ -90,7 +98,7 @@ def test_dense_mask_edges_bit_exact(case, sign):
                                       window_size=window, softmax_scale=needle_scale())
     vis = ref.dense_visible(Sq, Sk, causal, window)
     ve = ref._expand_kv(v, H)
-    for b in range(B):
+    for b in sorted({0, 1, B - 1} & set(range(B))):
         assert_equal_rows(out[b], needle_expected(ve[b], vis, sign), what=f"batch {b}")
 
 

@@ -15,6 +15,7 @@
 #include "fa_fwd_core.h"
 #include "fa_fwd_d128.h"
 #include "fa_fwd_1w.h"
+#include "fa_fwd_split.h"
 #include "fa_internal.h"
 
 namespace fa {
@@ -515,11 +516,33 @@ __global__ __launch_bounds__(256) void paged_combine_kernel(fa_paged_args a, int
 
 // ----------------------------------------------------------------- launchers
 
+// Keys split across the waves of a workgroup (fa_fwd_split.h): one
+// workgroup per 32 query rows of a head.
+template <class T, int D>
+static hipError_t launch_dense_split(const fa_fwd_args& a, int mode, hipStream_t st) {
+  using S = FwdSplitShape<D>;
+  const dim3 grid((unsigned)((a.seqlen_q + 31) / 32) * a.num_heads * a.batch),
+      block(64 * S::NW);
+  if (mode == kMaskCausal)
+    hipLaunchKernelGGL((fwd_split_kernel<T, D, kMaskCausal>), grid, block, 0, st, a);
+  else if (mode == kMaskBand)
+    hipLaunchKernelGGL((fwd_split_kernel<T, D, kMaskBand>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((fwd_split_kernel<T, D, kMaskNone>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 template <class T, int D>
 static hipError_t launch_dense(const fa_fwd_args& a, hipStream_t st) {
   using C = FwdKernelCfg<D, true>;
   const int qtiles = (a.seqlen_q + C::BM - 1) / C::BM;
   const int mode = mask_mode(a);
+  if constexpr (D == 64 || D == 128) {
+    // Too few query tiles to give most CUs a workgroup: split the keys.
+    const int64_t wgs = (int64_t)qtiles * a.num_heads * a.batch;
+    if (wgs * tiles::kFwdSplitMaxFillDen < (int64_t)device_cu_count() * tiles::kFwdSplitMaxFillNum)
+      return launch_dense_split<T, D>(a, mode, st);
+  }
   // Band instances run one workgroup per tile (fwd_dense_kernel).
   const bool band = mode == kMaskBand;
   const dim3 grid((unsigned)(band ? qtiles * a.num_heads * a.batch

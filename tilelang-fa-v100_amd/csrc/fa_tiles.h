@@ -44,11 +44,27 @@ constexpr int kFwd256Rows = 128;
 // Evidence (compiler resource usage): D = 64 takes 182 VGPRs and D = 256
 // 254 VGPRs + 152 AGPRs (one wave per SIMD), both without spills; D = 512
 // (two O passes) 253 VGPRs + 160 AGPRs in the VGPR MFMA form fa_fwd.hip is
-// built in (35 spilled in the default form).  C1 (D = 64) is launch-bound
-// (13.5 us), so its tile is sized for occupancy, not peak rate.
+// built in (35 spilled in the default form).  Dense problems too small to
+// give half the CUs a 128-row tile (C1) take the key-split kernel below.
 constexpr int kFwdCoreRows = 128;
 constexpr int kFwdCoreTileElems = 8192;  // keys x head_dim per K tile (D <= 256)
 constexpr int kFwdCoreKeys512 = 32;
+
+// ---- dense forward with keys split across the waves of a workgroup
+// (fa_fwd_split.h), head_dim 64 / 128: used when the standard cores' grid
+// would give fewer than a kFwdSplitMaxFill share of the CUs a workgroup
+// (configs[0], [1, 512, 16, 64]: 64 workgroups of 128 rows for 256 CUs).
+// 32 query rows per workgroup; 8 waves (two per SIMD), each with a private
+// pair of 32-key K / V tiles (double-buffered at head_dim 64, single at 128;
+// 128 KB of LDS).  Evidence (event time per call, same box): C1 9.2 us
+// against 13.5 us on the 128-row core (kernel trace 7.4 against 12.5 us) and
+// 10.9 us with 16 waves (one tile each, single-buffered); [1, 2048, 8, 128]
+// 43.0 / 33.2 us (full / causal) against 47.8 / 36.6 us with 4 waves and
+// 57.4 / 55.0 us on the 256-row core; [4, 300, 8, 128] 18.6 us against 16.6
+// (4 waves) and 18.9 (256-row core).
+constexpr int kFwdSplitWaves64 = 8;
+constexpr int kFwdSplitWaves128 = 8;
+constexpr int kFwdSplitMaxFillNum = 1, kFwdSplitMaxFillDen = 2;  // one half
 
 // ---- backward dK / dV kernel, head_dim 128 / 256 (fa_bwd_mfma.h)
 // KV-stationary: head_dim 128 keeps 256 keys per workgroup (8 waves x 32 keys,
