@@ -398,7 +398,8 @@ def extras(fa, dev, reps):
         del c, qd
 
     # Decode at the other head dims (64 sequences, 32 / 8 heads, fp16).
-    for name, D, n in (("decode_D64_64x16k", 64, 16384), ("decode_D256_64x8k", 256, 8192)):
+    for name, D, n in (("decode_D64_64x16k", 64, 16384), ("decode_D256_64x8k", 256, 8192),
+                       ("decode_D512_64x4k", 512, 4096)):
         lens = [n] * 64
         c = paged_inputs([1] * 64, lens, [0] * 64, 32, 8, D, torch.float16, dev,
                          torch.Generator().manual_seed(0), device_values=True)

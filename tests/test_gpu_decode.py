@@ -59,6 +59,13 @@ def test_head_dims_pages_dtypes(D, page, dtype):
     check(make_case(3, [900, 17, 4096], 16, 4, D, page=page, dtype=dtype))
 
 
+@pytest.mark.parametrize("Hq,Hkv,page", [(32, 4, 16), (8, 8, 16), (16, 8, 64)])
+def test_head_dim_512_group_sizes(Hq, Hkv, page):
+    # Head_dim 512 on the streaming kernel at 8, 1 and 2 query heads per item;
+    # lengths end mid-tile and inside the first tile.
+    check(make_case(7, [1500, 9, 2048, 31], Hq, Hkv, 512, page=page))
+
+
 def test_scale_and_public_entry_point():
     q, kc, vc, bt, sl, page = make_case(4, [333, 2048], 16, 4, 128)
     check((q, kc, vc, bt, sl, page), scale=0.3)
@@ -89,7 +96,7 @@ def _device_paged(lens, Hq, Hkv, D, seed):
     return q, kc, vc, bt.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV)
 
 
-@pytest.mark.parametrize("lens_kind", ["uniform32k_b64", "skewed_b64", "uniform32k_b16"])
+@pytest.mark.parametrize("lens_kind", ["uniform32k_b64", "skewed_b64", "uniform32k_b16", "d512_4k_b64"])
 def test_long_splits_agree_with_paged_prefill(lens_kind):
     # Batches large enough for 1024- to 4096-key splits (64 x 32k keys: the
     # kernel doubles the launcher's 2048 to 4096; the skewed batch keeps
@@ -97,18 +104,21 @@ def test_long_splits_agree_with_paged_prefill(lens_kind):
     # decode output is checked against the paged prefill kernel (checked
     # against the oracle above and in test_gpu_paged.py) run as one query
     # token per sequence with prefix = len - 1: the same attention.
+    D = 128
     if lens_kind == "skewed_b64":
         lens = torch.randint(1024, 32769, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    elif lens_kind == "d512_4k_b64":
+        lens, D = [4096 - 7 * i for i in range(64)], 512
     else:
         lens = [32768] * (64 if lens_kind == "uniform32k_b64" else 16)
-    q, kc, vc, bt, sl = _device_paged(lens, 32, 8, 128, seed=11)
+    q, kc, vc, bt, sl = _device_paged(lens, 32, 8, D, seed=11)
     out = fa.tilelang_decode_forward(q, kc, vc, bt, sl)
     B = len(lens)
     qsl = torch.arange(B + 1, dtype=torch.int32, device=DEV)
     pfx = (sl - 1).to(torch.int32)
     ref_out, _ = fa.tilelang_paged_forward(q, kc, vc, bt, sl, qsl, pfx, causal=True)
-    assert_close(out, ref_out.view(B, 32, 128).float().cpu())
-    assert rel_l2(out, ref_out.view(B, 32, 128).float().cpu()) < 1e-2
+    assert_close(out, ref_out.view(B, 32, D).float().cpu())
+    assert rel_l2(out, ref_out.view(B, 32, D).float().cpu()) < 1e-2
 
 
 def test_v_cache_with_its_own_token_stride():

@@ -274,14 +274,13 @@ int decode_group_size(const fa_decode_args& a) {
   return 1;
 }
 
-// The streaming kernel (fa_decode_stream.h) covers head_dim 64 / 128 / 256
-// with pages of at least 16 keys, at most kMaxGroup query heads per item and
+// The streaming kernel (fa_decode_stream.h) covers head_dim 64 - 512 with
+// pages of at least 16 keys, at most kMaxGroup query heads per item and
 // token strides whose 16-row offsets fit its 32-bit lane offsets; other
-// shapes use decode_split_kernel.  (At head_dim 512 one tile's operands and
-// the 32 output blocks exceed a wave's registers: 289 spilled.)
+// shapes use decode_split_kernel.
 static bool use_stream(const fa_decode_args& a) {
   const int64_t lim = int64_t(1) << 26;
-  return a.head_dim <= 256 && a.page_size >= 16 && a.batch <= DecStream<128>::kMaxBatch &&
+  return a.page_size >= 16 && a.batch <= DecStream<128>::kMaxBatch &&
          decode_group_size(a) <= DecStream<128>::kMaxGroup && a.k_stride[1] >= 0 &&
          a.k_stride[1] < lim && a.v_stride[1] >= 0 && a.v_stride[1] < lim;
 }
@@ -291,6 +290,7 @@ static int stream_waves_per_cu(int D) {
   switch (D) {
     case 64: return DecStream<64>::kWavesPerCU;
     case 256: return DecStream<256>::kWavesPerCU;
+    case 512: return DecStream<512>::kWavesPerCU;
   }
   return DecStream<128>::kWavesPerCU;
 }
@@ -353,8 +353,8 @@ static hipError_t launch_decode_gb(const fa_decode_args& a, DecodeWs ws,
   const int G = a.num_heads / a.num_kv_heads;
   const int64_t items = (int64_t)ws.nsplit * (G / GB) * a.num_kv_heads * a.batch;
   if (items > 0) {  // max_seq_len == 0: the combine alone writes zeros
-    if (D <= 256 && use_stream(a)) {
-      using SD = DecStream<D <= 256 ? D : 128>;
+    if (use_stream(a)) {
+      using SD = DecStream<D>;
       const int64_t wgs = std::max<int64_t>(
           1, std::min<int64_t>((items + SD::kWavesPerWG - 1) / SD::kWavesPerWG,
                                (int64_t)device_cu_count() * SD::kWavesPerCU / SD::kWavesPerWG));

@@ -1,6 +1,6 @@
-// Persistent streaming split-KV decode for head_dim 64 / 128 / 256 and pages
-// of at least 16 keys (gfx950); head_dim 512 and smaller pages take the
-// chunked decode_split_kernel (fa_decode.hip).
+// Persistent streaming split-KV decode for head_dim 64 / 128 / 256 / 512 and
+// pages of at least 16 keys (gfx950); smaller pages take the chunked
+// decode_split_kernel (fa_decode.hip).
 //
 // Work item = (sequence b, KV head, group of GB query heads, split c), one
 // split being kSplit consecutive keys.  Items are numbered sequence-major,
@@ -291,30 +291,49 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
   const int ps_mask = a.page_size - 1;
   const unsigned last_page = (unsigned)(a.num_pages - 1);
   const int ks1 = (int)a.k_stride[1], vs1 = (int)a.v_stride[1];
+  const int64_t ks1b = 2 * (int64_t)ks1, vs1b = 2 * (int64_t)vs1;  // bytes
 
   // ---- per-lane constants.  DMA: instruction c fills rows RPD c + dl, lane
   // (dl = lane / LPR, pos = lane % LPR) chunk position pos with chunk
   // pos ^ swz(row); offsets in elements from the tile's first row.
   auto swz = [](int r) { return dec_swz(r) & S::kSwzMask; };
   const int dl = lane / LPR, pos = lane % LPR;
-  int kdma[S::kDmaPerTensor], vdma[S::kDmaPerTensor];
+  // Head_dim 512 (one wave per SIMD, O in the accumulation registers) has no
+  // VGPRs for offset tables: there the offsets below are formed at each use
+  // (kBig), the others are tables.
+  constexpr bool kBig = D == 512;
+  constexpr int NT = kBig ? 1 : S::kDmaPerTensor;
+  int kdma[NT], vdma[NT];
 #pragma unroll
-  for (int c = 0; c < S::kDmaPerTensor; ++c) {
+  for (int c = 0; c < NT; ++c) {
     const int r = RPD * c + dl;
     kdma[c] = r * ks1 + 8 * (pos ^ swz(r));
     vdma[c] = r * vs1 + 8 * (pos ^ swz(r));
   }
+  // DMA c of a tile (element offsets from its first row).  Head_dim 512: one
+  // row per instruction (RPD = 1, dl = 0, pos = lane).
+  auto kdma_at = [&](int c) {
+    if constexpr (kBig) return c * ks1 + 8 * (lane ^ swz(c)); else return kdma[c];
+  };
+  auto vdma_at = [&](int c) {
+    if constexpr (kBig) return c * vs1 + 8 * (lane ^ swz(c)); else return vdma[c];
+  };
   // LDS operand offsets within a ring slot.  K (A operand c of S^T): row l16,
   // chunk 4c + grp.  V^T (A operand of O^T, d block db): lane (k = l16, grp)
   // points at row 4 grp + k / 4, columns 16 db + 4 (k % 4) .. + 3, so that
   // the transpose read hands lane (l16, grp) V[4 grp + j][16 db + l16], j < 4.
-  int koff[D / 32], voff[D / 16];
+  // Head_dim 512: the swizzle acts on the low 4 chunk bits, so chunk 4c + grp
+  // of a row lands at 16((4c + grp) ^ sw) = 64(c ^ (sw >> 2)) + 16(grp ^
+  // (sw & 3)), i.e. koff(c) = koff(0) ^ 64c; likewise voff(db) = voff(0) ^
+  // 32db and qoff(c) = qoff(0) + 64c.
+  constexpr int NK = kBig ? 1 : D / 32, NV = kBig ? 1 : D / 16;
+  int koff[NK], voff[NV];
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) koff[c] = l16 * RB + 16 * ((4 * c + grp) ^ swz(l16));
+  for (int c = 0; c < NK; ++c) koff[c] = l16 * RB + 16 * ((4 * c + grp) ^ swz(l16));
   {
     const int r = 4 * grp + (l16 >> 2);
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
+    for (int db = 0; db < NV; ++db) {
       const int chunk = 2 * db + ((l16 & 3) >> 1);
       voff[db] = TK * RB + r * RB + 16 * (chunk ^ swz(r)) + 8 * (l16 & 1);
     }
@@ -322,9 +341,9 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
   // Query slot: row h (head h0 + h) holds its RB bytes unswizzled; the B
   // operand c of S^T for column l16 is chunk 4c + grp of row l16 (columns
   // >= GB read row 0 and are zeroed after the read).
-  int qoff[D / 32];
+  int qoff[NK];
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) qoff[c] = (l16 < GB ? l16 : 0) * RB + 16 * (4 * c + grp);
+  for (int c = 0; c < NK; ++c) qoff[c] = (l16 < GB ? l16 : 0) * RB + 16 * (4 * c + grp);
   const uint32_t ring_base = lds_addr(ring[wv][0]);
   const uint32_t q_base = lds_addr(qslot[wv][0]);
 
@@ -390,11 +409,29 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
     }
     char* kb = ring[wv][slot];
     char* vb = kb + TK * RB;
-    if (dr_n == TK - 1) {
+    if (kBig && dr_n == TK - 1) {
+      // Row c at a scalar row pointer stepped by the row stride (opaquely,
+      // so that it is not re-derived as a 64-bit product per row) plus the
+      // lane's 16-byte chunk, formed per issue from an opaque lane index
+      // (not hoisted into a table of addresses across the loop).
+      int lb = lane;
+      asm volatile("" : "+v"(lb));
+      const char* kp = reinterpret_cast<const char*>(kc_n);
+      const char* vp = reinterpret_cast<const char*>(vc_n);
 #pragma unroll
       for (int c = 0; c < S::kDmaPerTensor; ++c) {
-        ld16_lds_nt(kc_n + kdma[c], kb + 1024 * c);
-        ld16_lds_nt(vc_n + vdma[c], vb + 1024 * c);
+        const uint32_t vo = 16u * (uint32_t)(lb ^ swz(c));
+        ld16_lds_nt(kp + vo, kb + 1024 * c);
+        ld16_lds_nt(vp + vo, vb + 1024 * c);
+        kp += ks1b;
+        vp += vs1b;
+        asm volatile("" : "+s"(kp), "+s"(vp));
+      }
+    } else if (dr_n == TK - 1) {
+#pragma unroll
+      for (int c = 0; c < S::kDmaPerTensor; ++c) {
+        ld16_lds_nt(kc_n + kdma_at(c), kb + 1024 * c);
+        ld16_lds_nt(vc_n + vdma_at(c), vb + 1024 * c);
       }
     } else {  // last tile of the item: rows past its end repeat the last key
 #pragma unroll
@@ -423,7 +460,14 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
     if (q_item == cI) {
       // DMA issued with this item's first tile, before it: resident once
       // that tile has passed its wait.
-      lds_read_q<D>(q_base, qoff, qb);
+      if constexpr (kBig) {
+        int qo[D / 32];
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) qo[c] = qoff[0] + 64 * c;
+        lds_read_q<D>(q_base, qo, qb);
+      } else {
+        lds_read_q<D>(q_base, qoff, qb);
+      }
       q_item = -1;
     } else {
       // The slot holds a later item's rows: read this item's rows directly.
@@ -491,11 +535,18 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
     }
     // B operand of O^T: k slots 8 grp + j hold key 4 grp + j for j < 4 and
     // zero for j >= 4; the A operand repeats its 4 keys in the upper slots.
-    const u32x4 pb = {T::pack(p[0], p[1]), T::pack(p[2], p[3]), 0u, 0u};
+    if constexpr (kBig) {
+      // 16x16x16: the 4 keys of each operand exactly (no duplicated A).
+      const u32x2 pb2 = {T::pack(p[0], p[1]), T::pack(p[2], p[3])};
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
-      const u32x4 va = {vt[db].x, vt[db].y, vt[db].x, vt[db].y};
-      o[db] = T::mma16(va, pb, o[db]);
+      for (int db = 0; db < D / 16; ++db) o[db] = T::mma16k16(vt[db], pb2, o[db]);
+    } else {
+      const u32x4 pb = {T::pack(p[0], p[1]), T::pack(p[2], p[3]), 0u, 0u};
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        const u32x4 va = {vt[db].x, vt[db].y, vt[db].x, vt[db].y};
+        o[db] = T::mma16(va, pb, o[db]);
+      }
     }
     if (++ct == cit.ntiles) {
       finish_item();
@@ -522,8 +573,22 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
       // Pins the prepared addresses ahead of the wait (volatile asm keeps its
       // order; the compiler would otherwise sink the address work past it).
       asm volatile("" ::"s"(kc_n), "s"(vc_n), "s"(dr_n), "s"(q_src));
-      lds_read_tile<D, (PD - 1) * S::kDmaPerTile>(ring_base + s * S::kTileBytes, koff, voff, kr,
-                                                  vt);
+      if constexpr (kBig) {
+        // Offsets formed here (opaquely rewritten bases: not hoisted into
+        // tables across the loop).
+        int kb0 = koff[0], vb0 = voff[0];
+        asm volatile("" : "+v"(kb0), "+v"(vb0));
+        int ko[D / 32], vo[D / 16];
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) ko[c] = kb0 ^ (64 * c);
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) vo[db] = vb0 ^ (32 * db);
+        lds_read_tile<D, (PD - 1) * S::kDmaPerTile>(ring_base + s * S::kTileBytes, ko, vo, kr,
+                                                    vt);
+      } else {
+        lds_read_tile<D, (PD - 1) * S::kDmaPerTile>(ring_base + s * S::kTileBytes, koff, voff,
+                                                    kr, vt);
+      }
       issue(s);
       if (cI < I1) consume(kr, vt);
     }

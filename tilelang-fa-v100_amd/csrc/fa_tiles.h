@@ -111,7 +111,8 @@ constexpr size_t kBwdDsMaxBytes = size_t(4) << 30;
 constexpr int kBwd64Keys = 128;
 constexpr int kBwd64QueryRows = 64;
 
-// ---- decode, head_dim 64 / 128 / 256 (fa_decode_stream.h)
+// ---- decode, head_dim 64 / 128 / 256 / 512, pages of at least 16 keys
+// (fa_decode_stream.h)
 // Persistent waves; work item = a split of keys x one KV head x its query
 // heads (up to 8, the 16x16x32 MFMA columns); 16-key tiles, two in flight
 // per wave.  Keys per split: the largest of kDecSplitKeysMax, /2, /4 ..
@@ -126,18 +127,18 @@ constexpr int kBwd64QueryRows = 64;
 // 1.006x its algorithmic bytes (FETCH_SIZE).  Head_dim 64 and 256 run the same
 // kernel with the ring depth and waves per workgroup scaled so that every CU
 // keeps ~128 KB of K / V in flight (64: 4 tiles x 8 waves, 256: 2 tiles x 4
-// waves): 64 x 16k keys at D = 64 76.0%, 64 x 8k at D = 256 83.2% of 8 TB/s,
-// against 63-66% on the chunked kernel below.
+// waves, 512: 2 tiles x 2 waves): 64 x 16k keys at D = 64 76.0%, 64 x 8k at
+// D = 256 83.2%, 64 x 4k at D = 512 79.2% of 8 TB/s, against 63-66% on the
+// chunked kernel below.
 constexpr int kDecSplitKeysMax = 2048;
 constexpr int kDecSplitKeysMin = 512;
 constexpr int kDecItemsPerWave = 2;
 constexpr int kDecTileKeys = 16;
 constexpr int kDecTilesInFlight = 2;
 
-// ---- decode, head_dim 512 and pages of fewer than 16 keys (fa_decode.hip):
-// 32768 elements (64 KB) of K per chunk, i.e. 32768 / D keys.  (The
-// streaming kernel at head_dim 512 spills 289 registers.)  64 x 4k keys at
-// D = 512: 63.8% of 8 TB/s.
+// ---- decode, pages of fewer than 16 keys (fa_decode.hip): 32768 elements
+// (64 KB) of K per chunk, i.e. 32768 / D keys.  64 x 4k keys at D = 512 (16-key
+// pages, before the streaming kernel took them): 63.8% of 8 TB/s.
 constexpr int kDecChunkElems = 32768;
 
 // ---- split-KV paged prefill (fa_fwd.hip paged_num_splits): no split when
