@@ -378,9 +378,10 @@ template <class T, int D>
 static hipError_t launch_bwd_ds(const fa_bwd_args& a, int mode, void* ws, hipStream_t st) {
   float* stats = static_cast<float*>(ws);
   uint16_t* ds = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + ds_offset(a));
-  const int64_t waves = (int64_t)a.batch * a.num_heads * ((a.seqlen_q + 31) / 32);
-  hipLaunchKernelGGL((bwd_stats_kernel<T, D>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
-                     st, a, stats);
+  const int64_t blocks = (int64_t)a.batch * a.num_heads * ((a.seqlen_q + 31) / 32);
+  constexpr int per_wg = 4 * StatsShape<D>::kTiles;  // 32-row blocks per workgroup
+  hipLaunchKernelGGL((bwd_stats_kernel<T, D>), dim3((unsigned)((blocks + per_wg - 1) / per_wg)),
+                     dim3(256), 0, st, a, stats);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_bwd_main<T, D>(a, mode, stats, ds, st);

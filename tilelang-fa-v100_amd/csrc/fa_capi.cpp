@@ -142,13 +142,14 @@ static int check_bwd(const fa_bwd_args* a) {
   }
   if (a->has_window && (a->window_left < -1 || a->window_right < -1))
     return fail(FA_E_INVALID, "fa_bwd: window sizes must be >= -1");
-  // Every grid is one-dimensional: at most one workgroup (or, for the row
-  // statistics, one wave) per 32 rows or keys of each (batch, head), and the
-  // kernels index (batch, head) pairs with 32-bit integers.
+  // Every grid is one-dimensional: at most one workgroup per 32 rows or keys
+  // of each (batch, head), and the kernels index (batch, head, 32-row block)
+  // with 32-bit integers (the row statistics' waves round that count up to a
+  // multiple of 16: the margin keeps those indices in range).
   const int64_t bh = (int64_t)a->batch * a->num_heads;
   const int64_t blocks32 = ((int64_t)std::max(a->seqlen_q, a->seqlen_k) + 31) / 32;
   const int64_t rows = bh * a->seqlen_q;
-  if (bh * std::max<int64_t>(blocks32, 1) > kIntMax || rows / 16 > kIntMax)
+  if (bh * std::max<int64_t>(blocks32, 1) > kIntMax - 64 || rows / 16 > kIntMax)
     return fail(FA_E_UNSUPPORTED, "fa_bwd: problem too large");
   return ok();
 }
