@@ -54,7 +54,13 @@ def test_group_sizes(Hq, Hkv):
 
 @pytest.mark.parametrize("D,page,dtype", [(64, 16, torch.float16), (256, 32, torch.float16),
                                           (128, 16, torch.bfloat16), (128, 1, torch.float16),
-                                          (512, 16, torch.float16), (512, 32, torch.bfloat16)])
+                                          (512, 16, torch.float16), (512, 32, torch.bfloat16),
+                                          # pages under 16 keys on the streaming kernel
+                                          (128, 8, torch.float16), (128, 4, torch.bfloat16),
+                                          (64, 8, torch.float16), (256, 2, torch.float16),
+                                          (512, 1, torch.float16), (512, 8, torch.bfloat16),
+                                          # and on the chunked kernel
+                                          (64, 4, torch.float16), (128, 2, torch.float16)])
 def test_head_dims_pages_dtypes(D, page, dtype):
     check(make_case(3, [900, 17, 4096], 16, 4, D, page=page, dtype=dtype))
 

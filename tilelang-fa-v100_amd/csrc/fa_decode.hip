@@ -275,12 +275,15 @@ int decode_group_size(const fa_decode_args& a) {
 }
 
 // The streaming kernel (fa_decode_stream.h) covers head_dim 64 - 512 with
-// pages of at least 16 keys, at most kMaxGroup query heads per item and
-// token strides whose 16-row offsets fit its 32-bit lane offsets; other
-// shapes use decode_split_kernel.
+// pages of at least 16 keys, or of at least the 1024 / 2D rows one of its
+// DMA instructions loads (8 keys at head_dim 64, 4 at 128, 2 at 256, 1 at
+// 512), at most kMaxGroup query heads per item and token strides whose
+// 16-row offsets fit its 32-bit lane offsets; other shapes use
+// decode_split_kernel.
 static bool use_stream(const fa_decode_args& a) {
   const int64_t lim = int64_t(1) << 26;
-  return a.page_size >= 16 && a.batch <= DecStream<128>::kMaxBatch &&
+  return (a.page_size >= 16 || a.page_size * 2 * a.head_dim >= 1024) &&
+         a.batch <= DecStream<128>::kMaxBatch &&
          decode_group_size(a) <= DecStream<128>::kMaxGroup && a.k_stride[1] >= 0 &&
          a.k_stride[1] < lim && a.v_stride[1] >= 0 && a.v_stride[1] < lim;
 }

@@ -1,5 +1,6 @@
 // Persistent streaming split-KV decode for head_dim 64 / 128 / 256 / 512 and
-// pages of at least 16 keys (gfx950); smaller pages take the chunked
+// pages of at least 16 keys, or of fewer when one DMA instruction's rows
+// (1024 / 2D) still fit a page (gfx950); smaller pages take the chunked
 // decode_split_kernel (fa_decode.hip).
 //
 // Work item = (sequence b, KV head, group of GB query heads, split c), one
@@ -362,7 +363,17 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
     const_i32_ptr bt = as_const(a.block_table) + (int64_t)it.b * a.block_table_stride;
     return bt[(it.n_begin + t * TK) >> ps_log2];
   };
-  int page_next = page_of(pit, 0);
+  // Pages of fewer than 16 keys (but at least RPD, so that each DMA
+  // instruction's RPD rows lie in one page): the page of instruction c's
+  // first row (clamped to the tile's last valid row), read in prepare() with
+  // a scalar load per instruction and used in issue(), after the tile wait
+  // (the loads' latency overlaps it).
+  const bool small = a.page_size < TK;
+  constexpr int NPG = S::kDmaPerTensor;
+  int pgr[NPG];
+#pragma unroll
+  for (int c = 0; c < NPG; ++c) pgr[c] = 0;
+  int page_next = small ? 0 : page_of(pit, 0);
   // Query slot: holds the rows of item q_item (-1: free).  Rows past GB
   // repeat row GB - 1 so that every DMA instruction stays in bounds.
   int q_item = -1;
@@ -382,12 +393,21 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
     }
     const int n = pit.n_begin + pt * TK;  // first key of the tile
     dr_n = min(TK - 1, pit.n_end - 1 - n);
-    const int64_t page = min((unsigned)page_next, last_page);
-    const int tok0 = n & ps_mask;  // tiles are 16-aligned and never cross a page
-    kc_n = static_cast<const uint16_t*>(a.k_cache) + (int64_t)pit.hk * a.k_stride[2] +
-           page * a.k_stride[0] + (int64_t)tok0 * ks1;
-    vc_n = static_cast<const uint16_t*>(a.v_cache) + (int64_t)pit.hk * a.v_stride[2] +
-           page * a.v_stride[0] + (int64_t)tok0 * vs1;
+    if (small) {
+      // Head bases only; the pages are applied per instruction in issue().
+      const_i32_ptr bt = as_const(a.block_table) + (int64_t)pit.b * a.block_table_stride;
+#pragma unroll
+      for (int c = 0; c < NPG; ++c) pgr[c] = bt[(n + min(RPD * c, dr_n)) >> ps_log2];
+      kc_n = static_cast<const uint16_t*>(a.k_cache) + (int64_t)pit.hk * a.k_stride[2];
+      vc_n = static_cast<const uint16_t*>(a.v_cache) + (int64_t)pit.hk * a.v_stride[2];
+    } else {
+      const int64_t page = min((unsigned)page_next, last_page);
+      const int tok0 = n & ps_mask;  // tiles are 16-aligned and never cross a page
+      kc_n = static_cast<const uint16_t*>(a.k_cache) + (int64_t)pit.hk * a.k_stride[2] +
+             page * a.k_stride[0] + (int64_t)tok0 * ks1;
+      vc_n = static_cast<const uint16_t*>(a.v_cache) + (int64_t)pit.hk * a.v_stride[2] +
+             page * a.v_stride[0] + (int64_t)tok0 * vs1;
+    }
     if (pdone) return;
     if (pt + 1 < pit.ntiles) {
       ++pt;
@@ -398,7 +418,7 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
       pdone = true;  // stays on the last tile
       return;
     }
-    page_next = page_of(pit, pt);
+    if (!small) page_next = page_of(pit, pt);
   };
   auto issue = [&](int slot) {
     if (q_src) {
@@ -409,7 +429,20 @@ void decode_stream_kernel(fa_decode_args a, DecodeWsS ws) {
     }
     char* kb = ring[wv][slot];
     char* vb = kb + TK * RB;
-    if (kBig && dr_n == TK - 1) {
+    if (small) {
+      // Instruction c: rows RPD c + dl of one page (the page of its first row
+      // clamped to the last valid one, dr_n); rows past dr_n repeat row dr_n.
+      // The tile starts a page (16-aligned), so row r sits at slot r & mask.
+#pragma unroll
+      for (int c = 0; c < S::kDmaPerTensor; ++c) {
+        const int r = RPD * c + dl;
+        const int64_t page = min((unsigned)pgr[c], last_page);
+        const int64_t slot = min(r, dr_n) & ps_mask;
+        const int j = 8 * (pos ^ swz(r));
+        ld16_lds_nt(kc_n + page * a.k_stride[0] + slot * ks1 + j, kb + 1024 * c);
+        ld16_lds_nt(vc_n + page * a.v_stride[0] + slot * vs1 + j, vb + 1024 * c);
+      }
+    } else if (kBig && dr_n == TK - 1) {
       // Row c at a scalar row pointer stepped by the row stride (opaquely,
       // so that it is not re-derived as a 64-bit product per row) plus the
       // lane's 16-byte chunk, formed per issue from an opaque lane index

@@ -111,8 +111,8 @@ constexpr size_t kBwdDsMaxBytes = size_t(4) << 30;
 constexpr int kBwd64Keys = 128;
 constexpr int kBwd64QueryRows = 64;
 
-// ---- decode, head_dim 64 / 128 / 256 / 512, pages of at least 16 keys
-// (fa_decode_stream.h)
+// ---- decode, head_dim 64 / 128 / 256 / 512, pages of at least 16 keys or of
+// at least one DMA instruction's 1024 / 2D rows (fa_decode_stream.h)
 // Persistent waves; work item = a split of keys x one KV head x its query
 // heads (up to 8, the 16x16x32 MFMA columns); 16-key tiles, two in flight
 // per wave.  Keys per split: the largest of kDecSplitKeysMax, /2, /4 ..
@@ -136,9 +136,10 @@ constexpr int kDecItemsPerWave = 2;
 constexpr int kDecTileKeys = 16;
 constexpr int kDecTilesInFlight = 2;
 
-// ---- decode, pages of fewer than 16 keys (fa_decode.hip): 32768 elements
-// (64 KB) of K per chunk, i.e. 32768 / D keys.  64 x 4k keys at D = 512 (16-key
-// pages, before the streaming kernel took them): 63.8% of 8 TB/s.
+// ---- decode, pages of fewer than 1024 / 2D keys (fa_decode.hip): 32768
+// elements (64 KB) of K per chunk, i.e. 32768 / D keys.  64 x 4k keys at
+// D = 512 (16-key pages, before the streaming kernel took them): 63.8% of
+// 8 TB/s; 64 x 16k keys at D = 128, pages of 1-8 keys: 65-67%.
 constexpr int kDecChunkElems = 32768;
 
 // ---- split-KV paged prefill (fa_fwd.hip paged_num_splits): no split when
