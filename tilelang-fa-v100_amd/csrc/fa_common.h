@@ -76,7 +76,9 @@ struct Half {
   }
   // Row-sum update for two probabilities p0, p1 whose packed form is w.
   // fp16 keeps 11 significant bits, so summing the rounded values (one
-  // v_dot2_f32_f16 with ones) moves the LSE by at most 2^-11.
+  // v_dot2_f32_f16 with ones) moves the LSE by at most 2^-11.  (The
+  // ping-pong head_dim 128 core sums the fp32 values instead: there the
+  // dot2 form overlaps the partner wave's matrix products worse.)
   __device__ __forceinline__ static float sum2(float, float, uint32_t w, float acc) {
     const f16x2 one = {(_Float16)1.f, (_Float16)1.f};
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);

@@ -438,7 +438,13 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
         const float p0 = fast_exp2(fmaf(s[kc >> 1][e], scale_log2, -mb));
         const float p1 = fast_exp2(fmaf(s[kc >> 1][e + 1], scale_log2, -mb));
         pb[kc][w] = T::pack(p0, p1);
-        l_run = T::sum2(p0, p1, pb[kc][w], l_run);
+        // The fp32 values, as the reference sums its fp32 scores
+        // (_kernels_forward.py:150-152).  The one-instruction fp16 form
+        // (T::sum2: v_dot2 of the packed pair) overlaps the partner wave's
+        // matrix products worse: T1 forward 0.545 -> 0.521 ms with the two
+        // adds (same box); a two-wave microbenchmark (one wave's MFMAs, the
+        // other's softmax instruction mix) shows the same.
+        l_run = l_run + (p0 + p1);
       }
   };
   // Oᵀ += Vᵀ Pᵀ (V from vb).
