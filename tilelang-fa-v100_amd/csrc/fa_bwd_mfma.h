@@ -95,6 +95,16 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
 
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[2];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[2];
+  // This lane's dK / dV rows (key kvw + lr), formed here and held in VGPRs:
+  // formed after the loop, their arguments (pointers and strides) stayed
+  // live through it as one 16-register scalar tuple, which spilled and was
+  // reloaded every iteration (16 v_readlane per tile; T1 backward 1.591 ->
+  // 1.547 ms, head_dim 256 1.535 -> 1.486 ms without them, same box).
+  uint16_t* dkp = static_cast<uint16_t*>(a.dk) + b * a.dk_stride[0] +
+                  (int64_t)(kvw + lr) * a.dk_stride[1] + hk * a.dk_stride[2];
+  uint16_t* dvp = static_cast<uint16_t*>(a.dv) + b * a.dv_stride[0] +
+                  (int64_t)(kvw + lr) * a.dv_stride[1] + hk * a.dv_stride[2];
+  asm volatile("" : "+v"(dkp), "+v"(dvp));
 
   // ---- K tile -> LDS: 1 KB blocks of RPB rows; wave w loads the blocks of
   // its own key rows.
@@ -421,12 +431,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     }
   }
 
-  const int my_kv = kvw + lr;
-  if (my_kv >= Sk) return;
-  uint16_t* dkp = static_cast<uint16_t*>(a.dk) + b * a.dk_stride[0] +
-                  (int64_t)my_kv * a.dk_stride[1] + hk * a.dk_stride[2];
-  uint16_t* dvp = static_cast<uint16_t*>(a.dv) + b * a.dv_stride[0] +
-                  (int64_t)my_kv * a.dv_stride[1] + hk * a.dv_stride[2];
+  if (kvw + lr >= Sk) return;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll

@@ -417,6 +417,35 @@ __device__ __forceinline__ void buffer_lds16_opaque(u32x4 rsrc, uint32_t voff, c
       : "v"(voff), "s"(rsrc), "s"(lds_addr(lds_block))
       : "memory");
 }
+// Four buffer_lds16_opaque DMAs from one resource (lane offsets v0..v3)
+// into the consecutive 1 KB blocks from lds_block on: one M0 value, stepped
+// by 1 KB between the instructions.  With one M0 value per block the
+// compiler held all of them (four per DMA site) in scalar registers and
+// spilled them; each DMA in the forward key loop then reloaded its M0 with a
+// v_readlane.
+__device__ __forceinline__ void buffer_lds16_x4(u32x4 rsrc, uint32_t v0, uint32_t v1, uint32_t v2,
+                                                uint32_t v3, const char* lds_block) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %6\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, 0x400\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, 0x400\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, 0x400\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %4, %5, 0 offen lds\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(rsrc), "s"(lds_addr(lds_block))
+      : "scc", "memory");
+}
 __device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_block) {
   uint32_t saved;
   asm volatile(

@@ -318,9 +318,11 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
     // not known to be); the resource must sit in scalar registers.
 #pragma unroll
     for (int w = 0; w < 4; ++w) rs[w] = __builtin_amdgcn_readfirstlane(rs[w]);
-#pragma unroll
-    for (int ii = 0; ii < DB; ++ii)
-      buffer_lds16_opaque(rs, kV ? v_loff[ii] : k_loff[ii], dst + (DB * wave + ii) * 1024);
+    // (T1 forward 0.525 -> 0.513 ms, C3 paged prefill 0.546 -> 0.529 ms
+    // against four single DMAs, same box.)
+    static_assert(DB == 4, "four 1 KB blocks per DMA wave");
+    const uint32_t* lo = kV ? v_loff : k_loff;
+    buffer_lds16_x4(rs, lo[0], lo[1], lo[2], lo[3], dst + DB * wave * 1024);
   };
 
   // This lane's Q row of the tile (P, row0), and (group A) its first K tile
