@@ -18,6 +18,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "fa355.h"
 #include "fa_tiles.h"
@@ -286,18 +287,17 @@ __device__ __forceinline__ int wave_sum_int(int x) {
 }
 
 // Epilogue of the forward cores for one valid row: the lane holds
-// o[dt][4g + i] = O[row][col0 + 32dt + 8g + 4lh + i] (unnormalised) and the row's
-// sum l_all and base-2 running max ms_run.  Writes O / l_all in the
-// input dtype and the natural-log LSE (Prob::kF32Out false), or, for
-// split-KV partials, O / l_all in fp32 and the base-2 LSE.  A row that saw
-// no key gets O = 0 and LSE = -inf.
-template <class T, int DT, class Prob>
-__device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
-                                              const f32x16 (&o)[DT], float l_all,
-                                              float ms_run, int col0 = 0) {
+// o[dt][4g + i] = O[row][32dt + 8g + 4lh + i] (unnormalised) and the row's
+// sum l_all and base-2 running max ms_run.  Writes O / l_all to op in the
+// input dtype and the natural-log LSE to lp (F32 false; lp nullptr: no LSE),
+// or, for split-KV partials, O / l_all in fp32 and the base-2 LSE (F32
+// true).  A row that saw no key gets O = 0 and LSE = -inf.
+template <class T, bool F32, int DT>
+__device__ __forceinline__ void fwd_store_ptrs(std::conditional_t<F32, float, uint16_t>* op,
+                                               float* lp, int lh, const f32x16 (&o)[DT],
+                                               float l_all, float ms_run) {
   const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
-  if constexpr (Prob::kF32Out) {
-    float* op = P.o32_ptr(row) + col0;
+  if constexpr (F32) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -306,9 +306,8 @@ __device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
                          o[dt][4 * g + 3] * inv};
         *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * g + 4 * lh) = w;
       }
-    if (lh == 0) *P.lse2_ptr(row) = l_all > 0.f ? ms_run + log2f(l_all) : neg_inf();
+    if (lh == 0) *lp = l_all > 0.f ? ms_run + log2f(l_all) : neg_inf();
   } else {
-    uint16_t* op = P.o_ptr(row) + col0;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -318,9 +317,34 @@ __device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
         w[1] = T::pack(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
         st8(op + 32 * dt + 8 * g + 4 * lh, w);
       }
-    if (P.has_lse && lh == 0)
-      *P.lse_ptr(row) = l_all > 0.f ? (ms_run + log2f(l_all)) * kLn2 : neg_inf();
+    if (lp != nullptr && lh == 0) *lp = l_all > 0.f ? (ms_run + log2f(l_all)) * kLn2 : neg_inf();
   }
+}
+
+// The row's output pointers (fwd_store_ptrs) of problem P: O from column
+// col0 on, and the LSE (nullptr when the problem stores none).
+template <class Prob>
+__device__ __forceinline__ auto fwd_out_ptr(const Prob& P, int row, int col0 = 0) {
+  if constexpr (Prob::kF32Out)
+    return P.o32_ptr(row) + col0;
+  else
+    return P.o_ptr(row) + col0;
+}
+template <class Prob>
+__device__ __forceinline__ float* fwd_lse_ptr(const Prob& P, int row) {
+  if constexpr (Prob::kF32Out)
+    return P.lse2_ptr(row);
+  else
+    return P.has_lse ? P.lse_ptr(row) : nullptr;
+}
+
+// fwd_store_ptrs with the pointers formed from P at the store.
+template <class T, int DT, class Prob>
+__device__ __forceinline__ void fwd_store_row(const Prob& P, int row, int lh,
+                                              const f32x16 (&o)[DT], float l_all,
+                                              float ms_run, int col0 = 0) {
+  fwd_store_ptrs<T, Prob::kF32Out>(fwd_out_ptr(P, row, col0), fwd_lse_ptr(P, row), lh, o, l_all,
+                                   ms_run);
 }
 
 // Instruction-scheduling hint for a loop of N steps that each issue L LDS

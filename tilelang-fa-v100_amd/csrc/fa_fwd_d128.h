@@ -359,6 +359,22 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
   const bool row_valid = row < nrows;
   const int my_lo = row_valid ? P.kv_lo(row) : 0;
   const int my_hi = row_valid ? P.kv_hi(row) : 0;
+  // Paged problems: the row's output pointers are formed here and held in
+  // VGPRs, so the arguments they come from (pointers, token and head
+  // strides) are not live through the key loop, where they spilled from
+  // the scalar registers (44 spilled SGPRs against 13; C3 paged prefill
+  // 0.5195 / 0.5149 -> 0.5135 / 0.5127 ms, C5 -0.5%, same box).  The dense
+  // core has no VGPRs to spare and forms them at the store.
+  constexpr bool kEarlyOut = !Prob::kRowStrided;
+  decltype(fwd_out_ptr(P, 0)) out_row = nullptr;
+  float* lse_row = nullptr;
+  if constexpr (kEarlyOut) {
+    if (row_valid) {
+      out_row = fwd_out_ptr(P, row);
+      lse_row = fwd_lse_ptr(P, row);
+    }
+    asm volatile("" : "+v"(out_row), "+v"(lse_row));
+  }
 
   f32x16 o[D / 32];
 #pragma unroll
@@ -539,7 +555,11 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
 
   // Every wave is past the loop's last barrier: LDS and qf are free.
   const float l_all = half_sum(l_run);
-  if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
+  if constexpr (kEarlyOut) {
+    if (row_valid) fwd_store_ptrs<T, Prob::kF32Out>(out_row, lse_row, lh, o, l_all, ms_run);
+  } else {
+    if (row_valid) fwd_store_row<T>(P, row, lh, o, l_all, ms_run);
+  }
   if (!next(P, row0)) break;
   start_tile();
   }
