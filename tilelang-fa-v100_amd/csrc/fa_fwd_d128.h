@@ -329,11 +329,18 @@ __device__ __forceinline__ void attn_fwd_tiles_d128(Prob P, int row0, float scal
   // into k0.
   u32x4 qf[D / 16];
   auto start_tile = [&]() {
-    const int rw = row0 + wave * 32 + lr;
+    // The lane index is formed afresh (an opaque v_mbcnt pair): held from
+    // the kernel's start, its 8 * lh offset was the one VGPR value the dense
+    // core spilled, and the reload's vmcnt(0) made the next tile's Q loads
+    // wait for the previous tile's output stores (S1k / S2k forward -1.2% to
+    // -1.8% without it, same box).
+    uint32_t ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int rw = row0 + wave * 32 + (int)(ln & 31);
     const bool valid = rw < P.nrows;
-    const uint16_t* qp = valid ? P.q_ptr(rw) : nullptr;
+    const uint16_t* qp = valid ? P.q_ptr(rw) + 8 * (int)(ln >> 5) : nullptr;
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) qf[c] = valid ? ld16(qp + 16 * c + 8 * lh) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < D / 16; ++c) qf[c] = valid ? ld16(qp + 16 * c) : u32x4{0, 0, 0, 0};
     const int hi = P.kv_hi(min(row0 + S::BM, P.nrows) - 1);
     const int lo = max(P.kv_lo(row0), 0) / BN * BN;
     if (lo < hi && !grp_b) issue_rows(hi, lo, k0, BoolC<false>{});
