@@ -228,6 +228,11 @@ DECODE = [
     ([100, 700], 8, 2, 128, 8, F16, 0),
     ([100, 700], 8, 2, 128, 64, BF16, 0),
     ([0, 37], 8, 2, 128, 16, F16, 0),                  # an empty sequence
+    # pages under 16 keys on the streaming kernel (one page per DMA instruction)
+    ([1, 3, 5, 17, 700, 3000], 8, 2, 128, 4, F16, 0),
+    ([129, 4000], 8, 2, 64, 8, BF16, 0),
+    ([7, 2500], 8, 2, 256, 2, F16, 0),
+    ([1, 1500], 4, 1, 512, 1, F16, 0),
 ]
 
 
