@@ -222,6 +222,33 @@ def profiled_traffic(name):
     return None
 
 
+def device_info(device):
+    """The box's own matrix rate next to the attention numbers.
+
+    Boxes of this pool run the same kernels up to ~13% apart in the
+    matrix-bound points (decode, HBM-bound, matches to ~1%): the shader clock
+    under sustained matrix load differs.  An fp16 8192^3 matrix product
+    through torch (hipBLASLt) is timed after the headline, so a reader can
+    tell a slow box from a slow kernel.
+    """
+    props = torch.cuda.get_device_properties(device)
+    a = torch.randn(8192, 8192, device=device, dtype=torch.float16)
+    b = torch.randn(8192, 8192, device=device, dtype=torch.float16)
+    for _ in range(3):
+        a @ b
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(10):
+        a @ b
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / 10
+    return {"name": props.name, "arch": getattr(props, "gcnArchName", "?"),
+            "compute_units": props.multi_processor_count,
+            "fp16_gemm_8192_tflops": round(2 * 8192 ** 3 / (ms * 1e-3) / 1e12, 1)}
+
+
 def clock_warmup(device, seconds=0.3):
     """Keeps the GPU busy with fp16 matrix products for `seconds`.
 
@@ -496,6 +523,7 @@ def main():
     if not args.no_extra:
         print("[bench] extra configs", file=sys.stderr, flush=True)
         extra.update(extras(fa, dev, args.reps))
+    device = device_info(dev)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -519,6 +547,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "device": device,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
