@@ -37,14 +37,18 @@ __device__ __forceinline__ void ds_store16(uint16_t* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
-// buffer_lds16_opaque with the non-temporal cache policy.
-__device__ __forceinline__ void buffer_lds16_stream(u32x4 rsrc, uint32_t voff, char* lds_block) {
+// buffer_lds16_opaque with the non-temporal cache policy, twice: bytes voff
+// and voff + 1024 of the resource into lds_block and lds_block + 1024, under
+// one M0 value (the instruction offset applies to the memory address and to
+// the LDS address alike).
+__device__ __forceinline__ void buffer_lds16_stream2(u32x4 rsrc, uint32_t voff, char* lds_block) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
       "buffer_load_dwordx4 %1, %2, 0 offen nt lds\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen offset:1024 nt lds\n\t"
       "s_nop 0\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
@@ -213,18 +217,23 @@ __global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_
   const uint16_t* ds_w =
       ds + 1024 * ((int64_t)bh * L.per_head() + L.prefix(min(qt, L.nq)));
   const u32x4 rs = rsrc_words(ds_w, (uint32_t)cnt * 2048u);
+  // K resource of the next step to issue (steps are issued in order), based
+  // at the wave's first row of that step and carried: one 64-bit add per
+  // step; num_records covers RW rows except where they run past Sk.
+  const uint32_t k_full = span_bytes(Sh::RW, a.k_stride[1], D);
+  u32x4 rk = rsrc_words(kg + (int64_t)(Sh::RW * wave) * a.k_stride[1], k_full);
+  const uint64_t k_step = 2ull * 32 * (uint64_t)a.k_stride[1];
   auto issue = [&](int s, int stage) {
     const int nb = 32 * s + Sh::RW * wave;
-    const int nvalid = max(min(Sh::RW, Sk - nb), 0);
-    const u32x4 rk = rsrc_words(kg + (int64_t)nb * a.k_stride[1],
-                                span_bytes(nvalid, a.k_stride[1], D));
+    u32x4 r = rk;
+    if (nb + Sh::RW > Sk) r[2] = span_bytes(max(min(Sh::RW, Sk - nb), 0), a.k_stride[1], D);
 #pragma unroll
     for (int i = 0; i < KBPW; ++i)
-      buffer_lds16_opaque(rk, k_loff[i], smem + stage * KTB + (KBPW * wave + i) * 1024);
-    const uint32_t so = (uint32_t)s * 2048u + 16u * lane;
-    char* sd = smem + OFF_S + stage * SSB + wave * 2048;
-    buffer_lds16_stream(rs, so, sd);
-    buffer_lds16_stream(rs, so + 1024u, sd + 1024);
+      buffer_lds16_opaque(r, k_loff[i], smem + stage * KTB + (KBPW * wave + i) * 1024);
+    const uint64_t p = (((uint64_t)rk[1]) << 32 | rk[0]) + k_step;
+    rk[0] = (uint32_t)p;
+    rk[1] = (uint32_t)(p >> 32);
+    buffer_lds16_stream2(rs, (uint32_t)s * 2048u + 16u * lane, smem + OFF_S + stage * SSB + wave * 2048);
   };
 
   // Transpose-read offsets.  A, read r, d tile dt: row 8(lane/32) + 4r +

@@ -201,8 +201,6 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
                           (int64_t)(hk * G) * a.do_stride[2] +
                           (int64_t)(max(it1, 1) - 1) * S::BQ * os1;
   const float* s_top = stats + 2 * head_rows * Sq + (max(it1, 1) - 1) * S::BQ;
-  const uint16_t* q_i = q_top;
-  const uint16_t* o_i = o_top;
   const float* s_i = s_top;
   // DS: the dS tile of the tile `step` computes next (same sweep order as
   // the issue side), stepped back by count(it) tiles per query tile.
@@ -215,20 +213,32 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
                           dsl.prefix(max(it1, 1) - 1) + kvw / 32);
   }
   uint16_t* ds_c = ds_top;
+  // Buffer resources of the tile to issue next, based at its first Q / dO
+  // row and carried from tile to tile: stepping back one tile is a 64-bit
+  // subtract of the base words, and num_records (bytes up to the end of the
+  // tile's last valid row) only differs on a head's first tile, the one that
+  // may end at row Sq (rows at or past Sq read as zero; their products are
+  // masked).  Built from the tile's row count every tile, the two resources
+  // took ~25 scalar instructions per tile.
+  const uint32_t q_full = span_bytes(S::BQ, qs1, D), o_full = span_bytes(S::BQ, os1, D);
+  const int n_first = min(Sq - (max(it1, 1) - 1) * S::BQ, S::BQ);
+  u32x4 rq = rsrc_words(q_top, span_bytes(n_first, qs1, D));
+  u32x4 ro = rsrc_words(o_top, span_bytes(n_first, os1, D));
+  auto step_back = [](u32x4& r, uint64_t bytes, uint32_t span) {
+    const uint64_t p = (((uint64_t)r[1]) << 32 | r[0]) - bytes;
+    r[0] = (uint32_t)p;
+    r[1] = (uint32_t)(p >> 32);
+    r[2] = span;
+  };
   auto issue_q = [&](int it, int qo, int oo, int so) {
     const int i0 = it * S::BQ;
-    // Buffer resources over the tile's valid rows: rows at or past Sq read
-    // as zero (their products are masked), so no row clamping is needed.
-    const uint32_t nrows = (uint32_t)min(Sq - i0, S::BQ);
-    const u32x4 rq = rsrc_words(q_i, span_bytes(nrows, qs1, D));
-    const u32x4 ro = rsrc_words(o_i, span_bytes(nrows, os1, D));
     // Opaque DMA: the loop's wait_vmem + barrier is the only wait the tile
-    // needs.
+    // needs.  The dO tile sits QT_BYTES after the Q tile.
+    (void)oo;
 #pragma unroll
     for (int ii = 0; ii < BPW; ++ii) {
       const int blk = BPW * wave + ii;
-      buffer_lds16_opaque(rq, q_loff[ii], smem + qo + blk * 1024);
-      buffer_lds16_opaque(ro, o_loff[ii], smem + oo + blk * 1024);
+      buffer_lds16_pair<S::QT_BYTES>(rq, q_loff[ii], ro, o_loff[ii], smem + qo + blk * 1024);
     }
     if (wave == 0) {
       // Lanes 0-31 fetch LSE*log2(e), lanes 32-63 rowdot ([B*H][2][Sq]).
@@ -241,12 +251,12 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     if (it-- == it0) {
       it = it1 - 1;
       ++h_rel;
-      q_i = q_top + h_rel * a.q_stride[2];
-      o_i = o_top + h_rel * a.do_stride[2];
       s_i = s_top + 2 * h_rel * Sq;
+      rq = rsrc_words(q_top + h_rel * a.q_stride[2], span_bytes(n_first, qs1, D));
+      ro = rsrc_words(o_top + h_rel * a.do_stride[2], span_bytes(n_first, os1, D));
     } else {
-      q_i -= S::BQ * qs1;
-      o_i -= S::BQ * os1;
+      step_back(rq, 2ull * S::BQ * (uint64_t)qs1, q_full);
+      step_back(ro, 2ull * S::BQ * (uint64_t)os1, o_full);
       s_i -= S::BQ;
     }
   };

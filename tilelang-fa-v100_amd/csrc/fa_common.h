@@ -470,6 +470,26 @@ __device__ __forceinline__ void buffer_lds16_x4(u32x4 rsrc, uint32_t v0, uint32_
       : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(rsrc), "s"(lds_addr(lds_block))
       : "scc", "memory");
 }
+// Two buffer_lds16_opaque DMAs from two resources: (r0, v0) into lds_block
+// and (r1, v1) into lds_block + STEP, under one saved M0.
+template <int STEP>
+__device__ __forceinline__ void buffer_lds16_pair(u32x4 r0, uint32_t v0, u32x4 r1, uint32_t v1,
+                                                  const char* lds_block) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %5\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, %6\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %3, %4, 0 offen lds\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(v0), "s"(r0), "v"(v1), "s"(r1), "s"(lds_addr(lds_block)), "i"(STEP)
+      : "scc", "memory");
+}
 __device__ __forceinline__ void global_lds4_opaque(const void* src, void* lds_block) {
   uint32_t saved;
   asm volatile(
