@@ -178,19 +178,36 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
     k_loff[ii] = 2u * (rr * (uint32_t)a.k_stride[1] + 8 * c);
     v_loff[ii] = 2u * (rr * (uint32_t)a.v_stride[1] + 8 * c);
   }
+  const int j0 = max(wg_lo, 0) / BN;
+  const int j1 = (wg_hi + BN - 1) / BN;
+  // Tiles are issued in order (n0 = j0 BN, (j0 + 1) BN, ...), so the two
+  // resources are carried from tile to tile: one 64-bit add of the base
+  // words each, num_records recomputed only where the rows run past wg_hi.
+  const uint32_t k_full = span_bytes(WR, a.k_stride[1], D), v_full = span_bytes(WR, a.v_stride[1], D);
+  const int nb0 = j0 * BN + WR * wave;
+  u32x4 rk = rsrc_words(kg + (int64_t)nb0 * a.k_stride[1], k_full);
+  u32x4 rv = rsrc_words(vg + (int64_t)nb0 * a.v_stride[1], v_full);
+  auto step_rsrc = [](u32x4& r, uint64_t bytes) {
+    const uint64_t p = (((uint64_t)r[1]) << 32 | r[0]) + bytes;
+    r[0] = (uint32_t)p;
+    r[1] = (uint32_t)(p >> 32);
+  };
   auto issue_tile = [&](int n0, char* kb, char* vb) {
     const int nb = n0 + WR * wave;
-    const uint32_t nvalid = (uint32_t)max(min(WR, wg_hi - nb), 0);
-    const u32x4 rk = rsrc_words(kg + (int64_t)nb * a.k_stride[1],
-                                span_bytes(nvalid, a.k_stride[1], D));
-    const u32x4 rv = rsrc_words(vg + (int64_t)nb * a.v_stride[1],
-                                span_bytes(nvalid, a.v_stride[1], D));
+    u32x4 k = rk, v = rv;
+    if (nb + WR > wg_hi) {
+      const uint32_t nvalid = (uint32_t)max(min(WR, wg_hi - nb), 0);
+      k[2] = span_bytes(nvalid, a.k_stride[1], D);
+      v[2] = span_bytes(nvalid, a.v_stride[1], D);
+    }
 #pragma unroll
     for (int ii = 0; ii < S::BPW; ++ii) {
       const int blk = S::BPW * wave + ii;
-      buffer_lds16_opaque(rk, k_loff[ii], kb + blk * 1024);
-      buffer_lds16_opaque(rv, v_loff[ii], vb + blk * 1024);
+      buffer_lds16_opaque(k, k_loff[ii], kb + blk * 1024);
+      buffer_lds16_opaque(v, v_loff[ii], vb + blk * 1024);
     }
+    step_rsrc(rk, 2ull * BN * (uint64_t)a.k_stride[1]);
+    step_rsrc(rv, 2ull * BN * (uint64_t)a.v_stride[1]);
   };
 
   // One tile, as BN / 32 blocks of 32 keys: each block's scores, P / dS and
@@ -271,8 +288,6 @@ void bwd_dq_kernel(fa_bwd_args a, float* stats) {
 
   // Double-buffered tiles; the loop covers two tiles so that every LDS read
   // names one array pair while the DMA of the next tile targets the other.
-  const int j0 = max(wg_lo, 0) / BN;
-  const int j1 = (wg_hi + BN - 1) / BN;
   if (j0 < j1) issue_tile(j0 * BN, k0, v0);
   for (int j = j0; j < j1; j += 2) {
     wait_vmem();
