@@ -69,6 +69,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
                 OFF_O1 = OFF_Q1 + S::QT_BYTES;
   constexpr int OFF_K = OFF_O1 + S::QT_BYTES;
   static_assert(OFF_ST1 + 2 * S::BQ * 4 <= OFF_Q0 && OFF_K % 512 == 0, "LDS layout");
+  static_assert(OFF_O0 - OFF_Q0 == S::QT_BYTES && OFF_O1 - OFF_Q1 == S::QT_BYTES, "dO after Q");
   __shared__ __attribute__((aligned(16))) char smem[OFF_K + S::K_BYTES];
   char* const Ks = smem + OFF_K;
 
@@ -230,11 +231,12 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     r[1] = (uint32_t)(p >> 32);
     r[2] = span;
   };
-  auto issue_q = [&](int it, int qo, int oo, int so) {
+  // Q / dO / statistics DMA of query tile `it` into the buffer at qo (the
+  // dO tile sits QT_BYTES after the Q tile) and so.
+  auto issue_q = [&](int it, int qo, int so) {
     const int i0 = it * S::BQ;
     // Opaque DMA: the loop's wait_vmem + barrier is the only wait the tile
-    // needs.  The dO tile sits QT_BYTES after the Q tile.
-    (void)oo;
+    // needs.
 #pragma unroll
     for (int ii = 0; ii < BPW; ++ii) {
       const int blk = BPW * wave + ii;
@@ -410,14 +412,14 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
   };
   bool stored = false;
   if (ntot > 0) {
-    issue_q(ii, OFF_Q0, OFF_O0, OFF_ST0);
+    issue_q(ii, OFF_Q0, OFF_ST0);
     advance_issue(ih, ii);
   }
   for (int t = 0; t < ntot; t += 2) {
     wait_tile(stored);
     __syncthreads();
     if (t + 1 < ntot) {
-      issue_q(ii, OFF_Q1, OFF_O1, OFF_ST1);
+      issue_q(ii, OFF_Q1, OFF_ST1);
       advance_issue(ih, ii);
     }
     stored = step(ci, OFF_Q0, OFF_O0, OFF_ST0);
@@ -426,7 +428,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     wait_tile(stored);
     __syncthreads();
     if (t + 2 < ntot) {
-      issue_q(ii, OFF_Q0, OFF_O0, OFF_ST0);
+      issue_q(ii, OFF_Q0, OFF_ST0);
       advance_issue(ih, ii);
     }
     stored = step(ci, OFF_Q1, OFF_O1, OFF_ST1);
