@@ -267,6 +267,16 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
   // offsets of its Q, dO and statistics tiles.  Returns whether the wave
   // stored a dS tile (DS: two global stores, the wave's newest memory
   // operations).
+  // Causal / full attention: tile `it` (rows i0 .. i0 + BQ - 1) is active
+  // for this wave iff i0 >= act_lo (some row sees key kvw: kvw <= i0 + BQ - 1
+  // + off) and needs no mask iff unm_lo <= i0 <= unm_hi (every row sees the
+  // wave's last key, the wave's 32 keys and the tile's rows all exist): two
+  // comparisons per tile instead of the band tests.
+  const int wkv_last = min(kvw + 31, Sk - 1);
+  constexpr int kNever = 0x7fffffff, kAlways = -0x7fffffff;
+  const int act_lo = kvw >= Sk ? kNever : MODE == kMaskCausal ? kvw - (S::BQ - 1) - off : kAlways;
+  const int unm_lo = kvw + 32 > Sk ? kNever : MODE == kMaskCausal ? wkv_last - off : kAlways;
+  const int unm_hi = Sq - S::BQ;
   auto step = [&](int it, int qo, int oo, int so) -> bool {
     const char* qb = smem + qo;
     const char* ob = smem + oo;
@@ -280,8 +290,7 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     // runs such tiles through the masked path instead (P = 0): its two-sided
     // test makes the register allocator spill heavily, and they are at most
     // BKV / BQ tiles per workgroup.
-    const bool active =
-        (MODE != kMaskCausal || band.any(i0, i0 + S::BQ - 1, kvw, kvw + 31)) && kvw < Sk;
+    const bool active = MODE == kMaskBand ? kvw < Sk : i0 >= act_lo;
     if (!active) return false;
     f32x16 s, dp;
 #pragma unroll
@@ -298,9 +307,10 @@ void bwd_main_mfma_kernel(fa_bwd_args a, const float* stats, uint16_t* ds) {
     // issued between the products of chunk c (bounds register use).
     sched_pipeline<D / 16, 3, 2, 2>();
 
-    const int wkv_last = min(kvw + 31, Sk - 1);
-    const bool need_mask = (CAUSAL && !band.all(i0, i0 + S::BQ - 1, kvw, wkv_last)) ||
-                           (kvw + 32 > Sk) || (i0 + S::BQ > Sq);
+    const bool need_mask =
+        MODE == kMaskBand
+            ? !band.all(i0, i0 + S::BQ - 1, kvw, wkv_last) || (kvw + 32 > Sk) || (i0 + S::BQ > Sq)
+            : i0 < unm_lo || i0 > unm_hi;
     // P = exp2(S·scale·log2e − lse2), dS = P (dP·scale − scale·rowdot).  The
     // statistics hold scale·rowdot, so the scale costs nothing.  Element (g, r)
     // is query i0 + 8g + 4lh + r; on masked tiles it sees the lane's key iff
