@@ -285,23 +285,19 @@ __global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_
   // (every wave's part of the K tile landed; the stage of step s - 1 is
   // free), refill that stage with step s + NBUF - 1.
   constexpr int PER_STAGE = KBPW + 2;
-  static_assert((NBUF - 2) * PER_STAGE <= 12, "waits below");
+  static_assert(PER_STAGE == 3 || PER_STAGE == 4, "waits below");
+  static_assert(NBUF == 4, "stage arithmetic and waits below");
   for (int s = 0; s < NBUF - 1 && s < nsteps; ++s) issue(s, s);
-  int stage = 0;
   for (int s = 0; s < nsteps; ++s) {
-    switch (min(NBUF - 2, nsteps - 1 - s) * PER_STAGE) {
-      case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-      case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-      case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-      default: wait_vmem(); break;
-    }
+    if (s + 2 < nsteps)
+      __builtin_amdgcn_s_waitcnt(PER_STAGE == 3 ? 0x0F76 : 0x0F78);  // vmcnt(2 PER_STAGE)
+    else if (s + 1 < nsteps)
+      __builtin_amdgcn_s_waitcnt(PER_STAGE == 3 ? 0x0F73 : 0x0F74);  // vmcnt(PER_STAGE)
+    else
+      wait_vmem();
     __syncthreads();
-    if (s + NBUF - 1 < nsteps) issue(s + NBUF - 1, stage == 0 ? NBUF - 1 : stage - 1);
-    if (s < cnt) compute(stage);
-    stage = stage == NBUF - 1 ? 0 : stage + 1;
+    if (s + NBUF - 1 < nsteps) issue(s + NBUF - 1, (s + NBUF - 1) & (NBUF - 1));
+    if (s < cnt) compute(s & (NBUF - 1));
   }
   wait_vmem();
 
