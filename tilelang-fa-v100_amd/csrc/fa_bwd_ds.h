@@ -226,7 +226,9 @@ __global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_
   auto issue = [&](int s, int stage) {
     const int nb = 32 * s + Sh::RW * wave;
     u32x4 r = rk;
-    if (nb + Sh::RW > Sk) r[2] = span_bytes(max(min(Sh::RW, Sk - nb), 0), a.k_stride[1], D);
+    if (nb + Sh::RW > Sk)
+      r[2] = __builtin_amdgcn_readfirstlane(
+          span_bytes(max(min(Sh::RW, Sk - nb), 0), a.k_stride[1], D));
 #pragma unroll
     for (int i = 0; i < KBPW; ++i)
       buffer_lds16_opaque(r, k_loff[i], smem + stage * KTB + (KBPW * wave + i) * 1024);
@@ -288,16 +290,23 @@ __global__ __launch_bounds__(64 * DqDsShape<D>::NW, DqDsShape<D>::WPE) void bwd_
   static_assert(PER_STAGE == 3 || PER_STAGE == 4, "waits below");
   static_assert(NBUF == 4, "stage arithmetic and waits below");
   for (int s = 0; s < NBUF - 1 && s < nsteps; ++s) issue(s, s);
-  for (int s = 0; s < nsteps; ++s) {
-    if (s + 2 < nsteps)
-      __builtin_amdgcn_s_waitcnt(PER_STAGE == 3 ? 0x0F76 : 0x0F78);  // vmcnt(2 PER_STAGE)
-    else if (s + 1 < nsteps)
-      __builtin_amdgcn_s_waitcnt(PER_STAGE == 3 ? 0x0F73 : 0x0F74);  // vmcnt(PER_STAGE)
-    else
-      wait_vmem();
+  auto step = [&](int s) {
     __syncthreads();
     if (s + NBUF - 1 < nsteps) issue(s + NBUF - 1, (s + NBUF - 1) & (NBUF - 1));
     if (s < cnt) compute(s & (NBUF - 1));
+  };
+  // All but the last two steps leave two stages in flight: one fixed wait.
+  int s = 0;
+  for (; s + 2 < nsteps; ++s) {
+    __builtin_amdgcn_s_waitcnt(PER_STAGE == 3 ? 0x0F76 : 0x0F78);  // vmcnt(2 PER_STAGE)
+    step(s);
+  }
+  for (; s < nsteps; ++s) {
+    if (s + 1 < nsteps)
+      __builtin_amdgcn_s_waitcnt(PER_STAGE == 3 ? 0x0F73 : 0x0F74);  // vmcnt(PER_STAGE)
+    else
+      wait_vmem();
+    step(s);
   }
   wait_vmem();
 
