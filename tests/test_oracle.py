@@ -266,7 +266,7 @@ def test_merge_of_split_partials_equals_unsplit():
     torch.testing.assert_close(mo2, full_o, atol=1e-12, rtol=1e-12)
 
 
-def test_pair_counts_match_enumeration_and_survey_configs():
+def test_pair_counts_match_enumeration_and_benchmark_configs():
     for sq, sk, c in ((5, 7, True), (7, 5, True), (6, 6, False), (2048, 2048, True)):
         assert ref.dense_pairs(sq, sk, c) == int(ref.dense_visible(sq, sk, c).sum())
     assert ref.dense_pairs(2048, 2048, True) == 2_098_176
