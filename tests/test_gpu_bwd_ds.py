@@ -37,6 +37,17 @@ CASES = [
     (1, 500, 300, 2, 2, 256, True, torch.float16),      # Sq > Sk
     (2, 333, 200, 2, 1, 256, False, torch.float16),     # full attention, MQA
     (1, 1, 90, 2, 2, 256, True, torch.float16),         # one query row
+    # dQ-from-dS loop edges: 2, 3 and 4 key steps (the steady loop runs all
+    # but the last two; its two-step tail), full and causal.  bf16 only where
+    # every row sees many keys: with Sq > Sk a causal row near the top sees
+    # one or two keys, dP - rowdot cancels, and the rowdot of the bf16-rounded
+    # O alone moves dq by up to 5e-3 (fp64 check), above atol.
+    (1, 64, 64, 2, 2, 128, False, torch.float16),
+    (1, 96, 96, 2, 2, 128, False, torch.bfloat16),
+    (1, 128, 128, 2, 1, 128, True, torch.float16),
+    (1, 96, 96, 2, 2, 256, False, torch.float16),
+    (1, 128, 100, 2, 2, 256, True, torch.float16),
+    (1, 100, 128, 2, 2, 256, True, torch.bfloat16),
 ]
 
 
